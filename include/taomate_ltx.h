@@ -1,0 +1,168 @@
+/*
+ * taomate_ltx.h -- C ABI of the MI355X (gfx950) chunked causal LTX attention path.
+ *
+ * The reference (TaoMate `ltx_causal`) is pure PyTorch: its hot path is
+ * `attention_with_cache` (ltx_causal/transformer/kv_cache.py:1148-1547), which runs
+ * q/k RMSNorm -> SPLIT RoPE -> torch.cat(cache, new) -> SDPA.  Each entry point
+ * below replaces one of the PyTorch operations that path reaches; the reference
+ * function each one stands in for is cited next to it.
+ *
+ * Conventions (all entry points):
+ *   - plain device pointers, int64 element strides (not bytes), dtype enums;
+ *   - return 0 (LTX_OK) or a negative ltx_status; never throw, never allocate
+ *     device memory, never synchronise; work is enqueued on `stream`;
+ *   - the message of the last failure on the calling thread is ltx_last_error();
+ *   - tensors follow the reference's [B, L, H, D] layout with D contiguous;
+ *   - key/value "segments": the logical key sequence is the concatenation of up
+ *     to LTX_MAX_SEGMENTS device spans (anchor | memory | window... | current),
+ *     which is what `torch.cat([cached_k, k], 1)` (kv_cache.py:1487-1491) builds
+ *     physically in the reference; here the spans are read in place.
+ */
+#ifndef TAOMATE_LTX_H
+#define TAOMATE_LTX_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LTX_ABI_VERSION 1
+#define LTX_MAX_SEGMENTS 16
+
+typedef enum {
+  LTX_F32 = 0,
+  LTX_BF16 = 1,
+  LTX_F8E4M3 = 2 /* OCP float8_e4m3fn (max 448, no inf) */
+} ltx_dtype;
+
+typedef enum {
+  LTX_OK = 0,
+  LTX_EINVAL = -1,       /* bad pointer, shape, stride or dtype */
+  LTX_EUNSUPPORTED = -2, /* valid request this build has no kernel for */
+  LTX_ELAUNCH = -3       /* the HIP launch itself failed */
+} ltx_status;
+
+/* ABI version this library implements (LTX_ABI_VERSION). */
+int ltx_abi_version(void);
+
+/* Text of the last error raised on the calling thread ("" if none). */
+const char* ltx_last_error(void);
+
+/*
+ * RoPE cos/sin table, SPLIT layout [B, H, T, dim/(2H)].
+ * Replaces causal_precompute_freqs_cis (ltx_causal/rope/causal_rope.py:139-357),
+ * SPLIT branch (:323-341), for the video 3-D (F,H,W) grid (:258-288), the audio
+ * 1-D grid (:295-300) and the video-time 1-D grid (:302-306).
+ *   freq_idx: device float32[n_freq], the generate_freq_grid values
+ *             (causal_rope.py:45-80; n_freq = dim / (2*num_pos_dims)).
+ *   num_pos_dims 3: grid (grid_f, grid_h, grid_w); 1: grid_f only, is_audio picks
+ *   the audio (mel) or video (pixel-frame) time conversion.
+ *   max_pos_*: normalisers (reference defaults 20, 2048, 2048).
+ *   out_dtype: LTX_F32 or LTX_BF16 (values computed in float32, rounded once).
+ *   The B batch rows are identical copies (the reference builds one per batch).
+ */
+int ltx_rope_table(void* cos_out, void* sin_out, int out_dtype, const float* freq_idx,
+                   int64_t n_freq, int num_pos_dims, int64_t grid_f, int64_t grid_h,
+                   int64_t grid_w, int64_t start_frame, int is_audio, float max_pos_t,
+                   float max_pos_h, float max_pos_w, int64_t dim, int64_t num_heads,
+                   int64_t batch, void* stream);
+
+/*
+ * Fused full-row RMSNorm + SPLIT RoPE on q and k rows.
+ * Replaces, in order: q_norm/k_norm = nn.RMSNorm(H*D, eps)
+ * (ltx_causal/attention/causal_attention.py:105-106, applied at
+ * kv_cache.py:1406-1407) and apply_split_rotary_emb (causal_rope.py:102-132,
+ * called through CausalLTXAttention._apply_rope, causal_attention.py:326-338,
+ * at kv_cache.py:1415-1417).
+ *   x rows: [B, L, H*D] with (b_stride, l_stride) in elements, H*D contiguous.
+ *   The k output may point into a KV arena (that is the "append" of new keys).
+ *   gamma_*: [H*D] in `dtype`, or NULL for gamma = 1.
+ *   eps_* < 0 skips the norm (RoPE only); cos_* == NULL skips RoPE (norm only).
+ *   Tables: [Bt, H, T, D/2] in tab_dtype with strides (tb, th, tt) in elements;
+ *   tb may be 0 to broadcast one table row over the batch.
+ *   Rounding (bf16): (x * rsqrt(mean x^2 + eps)) * gamma in float32 -> round
+ *   (PyTorch's fused rms_norm); then x1*c -> round -> +/-(s*x2) in float32 ->
+ *   round (the mul / addcmul_ pair of causal_rope.py:121-126).
+ *   k_in == NULL processes q only.
+ */
+int ltx_qk_rmsnorm_rope(int dtype, int64_t B, int64_t H, int64_t D,
+                        const void* q_in, int64_t q_len, int64_t q_in_bs, int64_t q_in_ls,
+                        void* q_out, int64_t q_out_bs, int64_t q_out_ls,
+                        const void* gamma_q, float eps_q,
+                        const void* q_cos, const void* q_sin, int64_t q_tb, int64_t q_th,
+                        int64_t q_tt,
+                        const void* k_in, int64_t k_len, int64_t k_in_bs, int64_t k_in_ls,
+                        void* k_out, int64_t k_out_bs, int64_t k_out_ls,
+                        const void* gamma_k, float eps_k,
+                        const void* k_cos, const void* k_sin, int64_t k_tb, int64_t k_th,
+                        int64_t k_tt,
+                        int tab_dtype, void* stream);
+
+/*
+ * KV append into a preallocated arena (copy or fp8 quantise).
+ * Replaces _cat_cache / torch.cat (ltx_causal/transformer/kv_cache.py:394-398,
+ * block cache update :2642-2656): the new tokens are written once into their
+ * arena slots instead of reallocating the whole cache.
+ *   src: [B, L, H, D] `src_dtype` (LTX_BF16 or LTX_F32), strides (bs, ls, hs).
+ *   dst: [B, L, H, D] `dst_dtype` strides (bs, ls, hs). dst_dtype LTX_BF16 copies;
+ *   LTX_F8E4M3 quantises with one scale per (b, h, frame) of `frame_tokens`
+ *   tokens: scale = absmax / 448 (1 if absmax == 0), q = rne_sat(x / scale).
+ *   scales: float32 [B, H, n_frames] with strides (sbs, shs), frame index f
+ *   at scales[b*sbs + h*shs + f]; only used for LTX_F8E4M3. L must be a
+ *   multiple of frame_tokens for LTX_F8E4M3.
+ */
+int ltx_kv_append(int src_dtype, int dst_dtype, int64_t B, int64_t L, int64_t H,
+                  int64_t D, const void* src, int64_t s_bs, int64_t s_ls, int64_t s_hs,
+                  void* dst, int64_t d_bs, int64_t d_ls, int64_t d_hs, float* scales,
+                  int64_t sc_bs, int64_t sc_hs, int64_t frame_tokens, void* stream);
+
+/*
+ * Span gather (cache compaction).
+ * Replaces _slice_tensor/_slice_cache (taomate/inference/cache.py:28-56) and
+ * _slice_kv_tensor (taomate/inference/streaming_runtime.py:431-442) when a
+ * physically contiguous copy is wanted (eviction itself is index-only).
+ *   Copies n_spans token ranges src[:, starts[i]:starts[i]+lens[i]] back to back
+ *   into dst[:, 0:sum(lens)].  starts/lens are host arrays.  src and dst must
+ *   not overlap.  elem_bytes: 1 (fp8), 2 (bf16) or 4 (f32); D*elem_bytes must
+ *   be a multiple of 4.
+ */
+int ltx_kv_gather(int64_t elem_bytes, int64_t B, int64_t H, int64_t D, const void* src,
+                  int64_t s_bs, int64_t s_ls, int64_t s_hs, void* dst, int64_t d_bs,
+                  int64_t d_ls, int64_t d_hs, int64_t n_spans, const int64_t* starts,
+                  const int64_t* lens, void* stream);
+
+/*
+ * Flash attention forward over segmented keys.
+ * Replaces standard_attention_forward -> F.scaled_dot_product_attention
+ * (ltx_causal/attention/flex_attention_utils.py:225-276, called at
+ * kv_cache.py:1531): out = softmax(q k^T * scale + mask) v over the keys of all
+ * segments in order; no causal mask (causality is what the segments contain).
+ *   q, out: [B, Lq, H, D] bf16, strides (bs, ls, hs).  D in {64, 128}.
+ *   Segment i: k_ptrs[i], v_ptrs[i] point at its first token (b=0, h=0);
+ *   seg_lens[i] tokens; all segments share kv strides (bs, ls, hs).
+ *   kv_dtype LTX_BF16, or LTX_F8E4M3 with per-(b, h, frame) float32 scales:
+ *   k_scales[i], v_scales[i] for segment i, index b*sc_bs + h*sc_hs + (t/frame)
+ *   where t counts tokens from the segment start.
+ *   key_mask: NULL or float32 additive mask [B, Lk_total] with batch stride
+ *   mask_bs (the reference's `(m - 1) * finfo.max` padding mask,
+ *   ltx_causal/transformer/causal_model.py:551-562).
+ *   lse: NULL or float32 [B, H, Lq] natural-log sum-exp of the scaled logits.
+ *   scale <= 0 selects 1/sqrt(D) (SDPA's default).
+ *   Host arrays (k_ptrs, v_ptrs, seg_lens, scales) are read during the call only.
+ */
+int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t H, int64_t D,
+                       int64_t q_bs, int64_t q_ls, int64_t q_hs, int64_t n_segments,
+                       const void* const* k_ptrs, const void* const* v_ptrs,
+                       const int64_t* seg_lens, int64_t kv_bs, int64_t kv_ls,
+                       int64_t kv_hs, int kv_dtype, const float* const* k_scales,
+                       const float* const* v_scales, int64_t sc_bs, int64_t sc_hs,
+                       int64_t frame_tokens, const float* key_mask, int64_t mask_bs,
+                       void* out, int64_t o_bs, int64_t o_ls, int64_t o_hs, float* lse,
+                       float scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TAOMATE_LTX_H */

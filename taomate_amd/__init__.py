@@ -1,0 +1,35 @@
+"""taomate_amd: TaoMate's chunked causal LTX attention path, native on MI355X (gfx950).
+
+The public names mirror the reference's drop-in surface:
+
+* ``attention_with_cache``, ``standard_attention_forward``, ``CausalLTXAttention``
+  (ltx_causal/transformer/kv_cache.py:1148, ltx_causal/attention/flex_attention_utils.py:225,
+  ltx_causal/attention/causal_attention.py:61)
+* ``causal_precompute_freqs_cis``, ``apply_split_rotary_emb``, ``generate_freq_grid``
+  (ltx_causal/rope/causal_rope.py:45-357)
+* ``LayerKVCache``, ``KVCache``, ``init_kv_cache``, ``_cat_cache``
+  (ltx_causal/transformer/kv_cache.py:321-398, ltx_causal/wrapper.py:15)
+* ``retain_streaming_context``, ``cache_segments``, ``attach_segments``
+  (taomate/inference/cache.py), ``compute_av_blocks`` (mask_builder.py:102)
+
+All device math goes through ``lib/libtaomate_ltx.so`` (C ABI in
+``include/taomate_ltx.h``); importing works without it, the first kernel call
+raises ``NativeLibraryError`` if it was not built.
+"""
+from ._native import NativeCallError, NativeLibraryError
+from .attention import CausalLTXAttention, attention_with_cache, standard_attention_forward
+from .blocks import AVBlock, compute_aligned_audio_frames, compute_av_blocks, global_block_at_index
+from .cache import (attach_segments, cache_segments, prune_clean_kv_to_sink_recent,
+                    retain_streaming_context)
+from .kv_cache import (ArenaSpec, KVArena, KVArenaFull, KVCache, KVSpanView, LayerKVCache,
+                       _cat_cache, init_kv_cache)
+from .rope import CausalRopeType, apply_split_rotary_emb, causal_precompute_freqs_cis, generate_freq_grid
+
+__all__ = [
+    "NativeCallError", "NativeLibraryError", "CausalLTXAttention", "attention_with_cache",
+    "standard_attention_forward", "AVBlock", "compute_aligned_audio_frames", "compute_av_blocks",
+    "global_block_at_index", "attach_segments", "cache_segments", "prune_clean_kv_to_sink_recent",
+    "retain_streaming_context", "ArenaSpec", "KVArena", "KVArenaFull", "KVCache", "KVSpanView",
+    "LayerKVCache", "_cat_cache", "init_kv_cache", "CausalRopeType", "apply_split_rotary_emb",
+    "causal_precompute_freqs_cis", "generate_freq_grid",
+]

@@ -1,0 +1,256 @@
+"""Drop-in attention surface on gfx950 kernels.
+
+Host mirror of:
+  CausalLTXAttention            ltx_causal/attention/causal_attention.py:61-338
+  standard_attention_forward    ltx_causal/attention/flex_attention_utils.py:225-276
+  attention_with_cache          ltx_causal/transformer/kv_cache.py:1148-1547 (single GPU)
+  _finish_attention_output...   ltx_causal/transformer/kv_cache.py:1680-1700
+
+Projections (to_q/to_k/to_v/to_out, to_gate_logits) stay ``nn.Linear`` GEMMs on
+PyTorch-ROCm (hipBLASLt).  Everything between them runs in this package's HIP
+kernels: fused full-row q/k RMSNorm + SPLIT RoPE (writing new keys straight into
+their KV-arena slots), the V append, and flash attention over the cached spans
+plus the new chunk.  Activations are bf16, as on the reference's GPU path.
+"""
+from __future__ import annotations
+
+from typing import List, Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+from . import kernels
+from .kernels import KVSegment
+from .kv_cache import KVSpanView
+from .rope import CausalRopeType, apply_split_rotary_emb
+
+
+class CausalLTXAttention(nn.Module):
+    """causal_attention.py:61-118: weight-compatible module (same attribute names)."""
+
+    def __init__(self, query_dim: int, context_dim: Optional[int] = None, heads: int = 8,
+                 dim_head: int = 64, norm_eps: float = 1e-6,
+                 rope_type: CausalRopeType = CausalRopeType.SPLIT,
+                 apply_gated_attention: bool = False, local_attn_size: int = -1,
+                 sink_size: int = 1):
+        super().__init__()
+        self.rope_type = rope_type
+        self.heads = heads
+        self.dim_head = dim_head
+        self.inner_dim = heads * dim_head
+        self.is_cross_attention = context_dim is not None
+        context_dim = query_dim if context_dim is None else context_dim
+        self.to_q = nn.Linear(query_dim, self.inner_dim, bias=True)
+        self.to_k = nn.Linear(context_dim, self.inner_dim, bias=True)
+        self.to_v = nn.Linear(context_dim, self.inner_dim, bias=True)
+        self.q_norm = nn.RMSNorm(self.inner_dim, eps=norm_eps)
+        self.k_norm = nn.RMSNorm(self.inner_dim, eps=norm_eps)
+        self.to_gate_logits = nn.Linear(query_dim, heads, bias=True) if apply_gated_attention else None
+        self.to_out = nn.Sequential(nn.Linear(self.inner_dim, query_dim, bias=True), nn.Identity())
+
+    def _apply_rope(self, x: torch.Tensor, freqs_cis: Tuple[torch.Tensor, torch.Tensor]) -> torch.Tensor:
+        """causal_attention.py:326-338 (SPLIT only)."""
+        if self.rope_type != CausalRopeType.SPLIT:
+            raise NotImplementedError("only SPLIT RoPE is built")
+        return apply_split_rotary_emb(x, *freqs_cis)
+
+    def forward(self, x: torch.Tensor, context: Optional[torch.Tensor] = None,
+                mask: Optional[torch.Tensor] = None, pe=None, k_pe=None, block_mask=None,
+                cross_causal_mask=None, logit_log_scale: Optional[torch.Tensor] = None,
+                sp_context_sharded: bool = True) -> torch.Tensor:
+        """causal_attention.py:120-324 on the inference path (no block masks, SP off).
+
+        This is the route text cross-attention takes (kv_cache.py:764-785): q/k
+        norm, optional RoPE, an optional key-padding mask, gate and to_out.
+        """
+        if block_mask is not None or cross_causal_mask is not None:
+            raise NotImplementedError("training block masks are not part of the inference path")
+        B = x.shape[0]
+        ctx = x if context is None else context
+        q_lin, k_lin, v = self.to_q(x), self.to_k(ctx), self.to_v(ctx)
+        q, k = _norm_rope(self, q_lin, k_lin, pe, k_pe, None)
+        if logit_log_scale is not None:
+            q = q * logit_log_scale
+        H, D = self.heads, self.dim_head
+        q4 = q.view(B, -1, H, D)
+        k4 = k.view(B, -1, H, D)
+        v4 = v.view(B, -1, H, D)
+        out = standard_attention_forward(q4, k4, v4, mask=mask)
+        return _finish(self, out, x)
+
+
+def _check_bf16(*ts):
+    for t in ts:
+        if t is not None and t.dtype != torch.bfloat16:
+            raise TypeError(f"the gfx950 attention path runs bf16 activations, got {t.dtype}")
+
+
+def _norm_rope(attn: CausalLTXAttention, q_lin: torch.Tensor, k_lin: torch.Tensor, pe, k_pe,
+               k_out: Optional[torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor]:
+    """q = rope(q_norm(q_lin)), k = rope(k_norm(k_lin)) in one launch
+    (kv_cache.py:1406-1417).  ``k_out`` may be an arena slot view [B, L, H, D]."""
+    _check_bf16(q_lin, k_lin)
+    H, D = attn.heads, attn.dim_head
+    q = torch.empty_like(q_lin)
+    k = torch.empty_like(k_lin) if k_out is None else k_out
+    kp = k_pe if k_pe is not None else pe
+    gq = attn.q_norm.weight if attn.q_norm.weight is not None else None
+    gk = attn.k_norm.weight if attn.k_norm.weight is not None else None
+    _check_bf16(gq, gk)
+    eq = attn.q_norm.eps if attn.q_norm.eps is not None else torch.finfo(q_lin.dtype).eps
+    ek = attn.k_norm.eps if attn.k_norm.eps is not None else torch.finfo(k_lin.dtype).eps
+    kernels.qk_rmsnorm_rope(q_lin, q, gq, eq, pe, H, D, k_lin, k, gk, ek, kp)
+    return q, k
+
+
+def _finish(attn: CausalLTXAttention, out: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """kv_cache.py:1680-1700: reshape, optional per-head gate 2*sigmoid(.), to_out."""
+    B = x.shape[0]
+    out = out.reshape(B, -1, attn.inner_dim)
+    if attn.to_gate_logits is not None:
+        g = attn.to_gate_logits(x)
+        b, t, _ = out.shape
+        out = (out.view(b, t, attn.heads, attn.dim_head) * (2.0 * torch.sigmoid(g)).unsqueeze(-1))
+        out = out.view(b, t, attn.inner_dim)
+    return attn.to_out(out)
+
+
+def _key_padding_mask(mask: Optional[torch.Tensor], B: int, Lk: int) -> Optional[torch.Tensor]:
+    """Reduce the reference's mask forms (flex_attention_utils.py:250-264) to the
+    additive float32 [B or 1, Lk] key mask the kernel takes.  Masks that vary
+    per query are not on the inference path."""
+    if mask is None:
+        return None
+    m = mask
+    if m.dtype == torch.bool:
+        m = torch.zeros(m.shape, dtype=torch.float32, device=m.device).masked_fill_(~m, float("-inf"))
+    if m.ndim == 4:
+        if m.shape[1] != 1 or m.shape[2] != 1:
+            raise NotImplementedError("only key-padding masks [B,1,1,Lk] are supported")
+        m = m[:, 0, 0, :]
+    elif m.ndim == 3:
+        if m.shape[1] != 1:
+            raise NotImplementedError("only key-padding masks [B,1,Lk] are supported")
+        m = m[:, 0, :]
+    elif m.ndim == 2:
+        if m.shape[0] != 1 and m.shape[0] != B:
+            raise NotImplementedError("2-D masks must be [1 or B, Lk] key-padding masks")
+    else:
+        raise NotImplementedError(f"mask of shape {tuple(mask.shape)}")
+    if m.shape[-1] != Lk:
+        raise ValueError(f"mask covers {m.shape[-1]} keys, attention has {Lk}")
+    return m.to(torch.float32).contiguous()
+
+
+def standard_attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                               mask: Optional[torch.Tensor] = None,
+                               scale: Optional[float] = None) -> torch.Tensor:
+    """flex_attention_utils.py:225-276: [B, L, H, D] in, [B, L, H, D] out."""
+    _check_bf16(q, k, v)
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    qq = q if q.stride(3) == 1 else q.contiguous()
+    kk = k if k.stride(3) == 1 else k.contiguous()
+    vv = v if v.stride() == kk.stride() else v.contiguous()
+    if kk.stride() != vv.stride():
+        kk = kk.contiguous()
+        vv = vv.contiguous()
+    km = _key_padding_mask(mask, q.shape[0], k.shape[1])
+    kernels.flash_attn(qq, [KVSegment(kk, vv)], out, key_mask=km, scale=scale)
+    return out
+
+
+def _cached_segments(cached_k, cached_v) -> Tuple[List[KVSegment], int]:
+    """Key segments of the cache (arena spans or one dense tensor) and the
+    fp8 frame size (0 for bf16)."""
+    if cached_k is None:
+        return [], 0
+    if isinstance(cached_k, KVSpanView):
+        if not (isinstance(cached_v, KVSpanView) and cached_v.arena is cached_k.arena
+                and cached_v.spans == cached_k.spans):
+            raise ValueError("cached_k / cached_v must be views of one arena with equal spans")
+        segs = []
+        for (k, ks), (v, vs) in zip(cached_k.pieces(), cached_v.pieces()):
+            segs.append(KVSegment(k, v, ks, vs))
+        return segs, (cached_k.arena.frame_tokens if cached_k.arena.fp8 else 0)
+    _check_bf16(cached_k, cached_v)
+    return [KVSegment(cached_k, cached_v)], 0
+
+
+def attention_with_cache(
+    attn: CausalLTXAttention,
+    x: torch.Tensor,
+    context: Optional[torch.Tensor],
+    pe: Optional[Tuple[torch.Tensor, torch.Tensor]],
+    k_pe: Optional[Tuple[torch.Tensor, torch.Tensor]],
+    cached_k,
+    cached_v,
+    logit_log_scale: Optional[torch.Tensor] = None,
+    pyramid_policy=None,
+    layer_idx: Optional[int] = None,
+    modality: Optional[str] = None,
+    frame_seqlen: Optional[int] = None,
+    sp_context_sharded: bool = True,
+    new_kv_real_len: Optional[int] = None,
+    profile_name: Optional[str] = None,
+):
+    """kv_cache.py:1148-1547 (single-GPU synchronous branch).
+
+    Returns ``(out [B, L, Dq], new_k, new_v)``.  When ``cached_k``/``cached_v``
+    are arena views the new K/V are written into free arena slots and returned
+    as views, so ``_cat_cache(cached_k, new_k)`` is free; otherwise they are
+    dense [B, L_new, H, D] tensors as in the reference.  Keys attended are
+    cached (in order) followed by the new chunk, with no mask: causality is
+    what the cache holds (kv_cache.py:1525-1531).
+    """
+    if pyramid_policy is not None:
+        raise NotImplementedError("PyramidKVPolicy is never constructed on the inference path")
+    B, L, _ = x.shape
+    ctx = x if context is None else context
+    H, D = attn.heads, attn.dim_head
+    q_lin, k_lin, v_lin = attn.to_q(x), attn.to_k(ctx), attn.to_v(ctx)
+    _check_bf16(q_lin, k_lin, v_lin)
+    Lk_new = k_lin.shape[1]
+    real = Lk_new if new_kv_real_len is None else min(int(new_kv_real_len), Lk_new)
+    k_lin = k_lin[:, :real]
+    v_lin = v_lin[:, :real]
+
+    arena = cached_k.arena if isinstance(cached_k, KVSpanView) else None
+    segs, frame = _cached_segments(cached_k, cached_v)
+    if arena is not None and not arena.fp8:
+        slot = arena.alloc(real)
+        k_dst = arena.slots("k", slot, real)
+        q, _ = _norm_rope(attn, q_lin, k_lin, pe, k_pe, k_dst)
+        kernels.kv_append(v_lin.view(B, real, H, D), arena.slots("v", slot, real))
+        new_k = KVSpanView(arena, "k", [(slot, real)])
+        new_v = KVSpanView(arena, "v", [(slot, real)])
+        segs.append(KVSegment(k_dst, arena.slots("v", slot, real)))
+    elif arena is not None:
+        # fp8 arena: the new chunk is quantised into its slots and attended in fp8
+        q, k = _norm_rope(attn, q_lin, k_lin, pe, k_pe, None)
+        slot = arena.alloc(real)
+        kd, vd = arena.slots("k", slot, real), arena.slots("v", slot, real)
+        ks, vs = arena.scale_slots("k", slot, real), arena.scale_slots("v", slot, real)
+        kernels.kv_append(k.view(B, real, H, D), kd, ks, arena.frame_tokens)
+        kernels.kv_append(v_lin.view(B, real, H, D), vd, vs, arena.frame_tokens)
+        new_k = KVSpanView(arena, "k", [(slot, real)])
+        new_v = KVSpanView(arena, "v", [(slot, real)])
+        segs.append(KVSegment(kd, vd, ks, vs))
+    else:
+        q, k = _norm_rope(attn, q_lin, k_lin, pe, k_pe, None)
+        new_k = k.view(B, real, H, D)
+        new_v = v_lin.view(B, real, H, D)
+        if not new_v.is_contiguous() or (segs and segs[0].k.stride() != new_k.stride()):
+            new_v = new_v.contiguous()
+            new_k = new_k.contiguous()
+        if segs and segs[0].k.stride() != new_k.stride():
+            # one dense cache tensor with other strides: attend cache ++ new densely
+            full_k = torch.cat([segs[0].k, new_k], dim=1)
+            full_v = torch.cat([segs[0].v, new_v], dim=1)
+            segs = [KVSegment(full_k, full_v)]
+        else:
+            segs.append(KVSegment(new_k, new_v))
+    if logit_log_scale is not None:
+        q = q * logit_log_scale
+    out = torch.empty(B, L, H, D, dtype=q.dtype, device=q.device)
+    kernels.flash_attn(q.view(B, L, H, D), segs, out, frame_tokens=frame)
+    return _finish(attn, out, x), new_k, new_v

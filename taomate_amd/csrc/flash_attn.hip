@@ -1,0 +1,527 @@
+// Flash-style attention forward for gfx950 (CDNA4) over segmented keys.
+//
+// Replaces F.scaled_dot_product_attention as reached through
+// standard_attention_forward (ltx_causal/attention/flex_attention_utils.py:225-276)
+// from attention_with_cache (ltx_causal/transformer/kv_cache.py:1531), whose keys
+// are torch.cat([cached_k, k], 1) (kv_cache.py:1487-1491).  Here the keys stay
+// where they live (anchor | memory | window | current spans of a KV arena) and
+// the kernel walks the spans in order.
+//
+// Work decomposition.  A workgroup of 4 wavefronts owns BM = 128 query rows of
+// one (batch, head); each wavefront owns 32 rows.  Keys stream through LDS in
+// tiles of BN = 64, double buffered: while the MFMAs consume tile j, the next
+// tile is already in registers (global loads issued one tile ahead).
+//
+// Matrix-core mapping (v_mfma_f32_32x32x16_bf16, lane l, i = l % 32, g = l / 32):
+//   S^T = K Q^T: A = K rows (LDS), B = Q^T (registers, loaded once).  The
+//   accumulator gives every lane ONE query (i) and 16 keys of each 32-key block,
+//   so the softmax row statistics are per-lane scalars plus a single exchange
+//   with lane l ^ 32, which holds the other 16 keys of the same query.
+//   K rows are stored in LDS with row-index bits 2 and 3 swapped; with that
+//   order accumulator register r of block kb holds key kb*32 + 16*(r/8) + 8g +
+//   r%8, i.e. each lane's 8-register half is 8 consecutive keys.
+//   O^T += V^T P^T: B = P straight from the softmax registers (8 consecutive
+//   keys per lane, as above), A = V^T read from a transposed V tile in LDS.
+//   The accumulator again gives each lane one query, so the online-softmax
+//   rescale is one scalar per lane.
+// Softmax: base-2 exponent with log2(e) folded into the logit scale
+// (exp(x) = 2^(x*log2 e)), running max / running sum per query (the online
+// normaliser of Milakov & Gimelshein 2018, as used by Dao et al. 2022).
+// fp8 KV: tiles are decoded to bf16 on their way into LDS; the per-(head,
+// frame) scales are folded into the logit scale (K) and into P (V).
+
+#include "ltx_common.h"
+
+namespace ltx {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+struct FlashParams {
+  const uint16_t* q;
+  uint16_t* o;
+  float* lse;
+  const float* mask;
+  int64_t q_bs, q_ls, q_hs;
+  int64_t o_bs, o_ls, o_hs;
+  int64_t kv_bs, kv_ls, kv_hs;
+  int64_t sc_bs, sc_hs;
+  int64_t mask_bs;
+  int64_t Lk;
+  int64_t seg_start[LTX_MAX_SEGMENTS + 1];
+  const void* k_ptr[LTX_MAX_SEGMENTS];
+  const void* v_ptr[LTX_MAX_SEGMENTS];
+  const float* k_sc[LTX_MAX_SEGMENTS];
+  const float* v_sc[LTX_MAX_SEGMENTS];
+  int tile_start[LTX_MAX_SEGMENTS + 1];  // first key tile of each segment (cumulative)
+  int B, H, Lq, n_seg, n_qtiles, frame;
+  float scale;       // softmax scale applied to q.k
+  float scale_log2;  // scale * log2(e)
+};
+
+constexpr int kBM = 128;
+constexpr int kBN = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Row r of a K tile is stored at LDS row sig(r): bits 2 and 3 swapped.
+__device__ __forceinline__ int sig(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+
+// Blocks are dispatched round-robin over the 8 XCDs (block id % 8).  Give each
+// XCD a contiguous range of the (batch*head, q-tile) space so the q-tiles that
+// share one head's K/V run on the same XCD and hit the same L2.
+__device__ __forceinline__ int xcd_remap(int bid, int nb) {
+  const int xcd = bid & 7, slot = bid >> 3;
+  const int per = nb >> 3, rem = nb & 7;
+  return xcd * per + (xcd < rem ? xcd : rem) + slot;
+}
+
+template <bool FP8>
+struct KVChunk;
+template <>
+struct KVChunk<false> {
+  using raw_t = uint4;  // 8 bf16
+  static __device__ __forceinline__ raw_t zero() { return make_uint4(0, 0, 0, 0); }
+  static __device__ __forceinline__ raw_t load(const void* base, int64_t off) {
+    return *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(base) + off);
+  }
+  static __device__ __forceinline__ raw_t bload(__amdgpu_buffer_rsrc_t r, int off) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+  }
+  static __device__ __forceinline__ uint4 to_bf16(raw_t r) { return r; }
+};
+template <>
+struct KVChunk<true> {
+  using raw_t = uint2;  // 8 fp8
+  static __device__ __forceinline__ raw_t zero() { return make_uint2(0, 0); }
+  static __device__ __forceinline__ raw_t load(const void* base, int64_t off) {
+    return *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(base) + off);
+  }
+  static __device__ __forceinline__ raw_t bload(__amdgpu_buffer_rsrc_t r, int off) {
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    return make_uint2(v[0], v[1]);
+  }
+  // Exact: every e4m3 value is representable in bf16.
+  static __device__ __forceinline__ uint4 to_bf16(raw_t r) {
+    uint32_t w[2] = {r.x, r.y};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], false);
+      f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], true);
+      o[2 * i] = (__float_as_uint(lo[0]) >> 16) | (__float_as_uint(lo[1]) & 0xFFFF0000u);
+      o[2 * i + 1] = (__float_as_uint(hi[0]) >> 16) | (__float_as_uint(hi[1]) & 0xFFFF0000u);
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+  }
+};
+
+// Key tiles never cross a segment: each segment is cut into ceil(len / kBN)
+// tiles (the last one partial).  The iterator walks them in order with
+// wave-uniform (scalar) state, touching the per-segment kernel arguments only
+// when it enters a new segment.
+struct TileIter {
+  int s;
+  int64_t row0;  // first token of the tile inside segment s
+  int64_t len;   // tokens in segment s
+  int64_t key0;  // first token of the tile in the concatenated key sequence
+  const void* k;
+  const void* v;
+
+  __device__ __forceinline__ void enter(const FlashParams& p, int seg) {
+    s = seg;
+    row0 = 0;
+    key0 = p.seg_start[seg];
+    len = p.seg_start[seg + 1] - key0;
+    k = p.k_ptr[seg];
+    v = p.v_ptr[seg];
+  }
+  __device__ __forceinline__ void next(const FlashParams& p) {
+    row0 += kBN;
+    key0 += kBN;
+    if (row0 >= len && s + 1 < p.n_seg) enter(p, s + 1);
+  }
+  __device__ __forceinline__ int nvalid() const {
+    return (int)(len - row0 < kBN ? len - row0 : kBN);
+  }
+};
+
+template <int D, bool FP8, bool MASK>
+__global__ void __launch_bounds__(256, 2) flash_fwd_kernel(const FlashParams p) {
+  constexpr int BM = kBM, BN = kBN;
+  constexpr int KS = D + 8;                // K tile LDS row stride (elements)
+  constexpr int VS = BN + 8;               // V^T tile LDS row stride
+  constexpr int KBUF = BN * KS;
+  constexpr int VBUF = D * VS;
+  constexpr int NKC = D / 8;               // 8-element chunks per K row
+  constexpr int KROWS_PER_PASS = 256 / NKC;
+  constexpr int K_LOADS = BN / KROWS_PER_PASS;
+  constexpr int NVP = (BN / 4) * (D / 8);  // (4-key group, 8-d chunk) pairs
+  constexpr int DB = D / 32;
+  constexpr int QS = D / 16;
+  using Chunk = KVChunk<FP8>;
+  using raw_t = typename Chunk::raw_t;
+
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (KBUF + VBUF)];
+  __shared__ float mask_s[MASK ? 2 : 1][MASK ? BN : 1];
+
+  const int linear = xcd_remap(blockIdx.x, gridDim.x);
+  const int qt = linear % p.n_qtiles;
+  const int bh = linear / p.n_qtiles;
+  const int b = bh / p.H, h = bh % p.H;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int li = lane & 31, hg = lane >> 5;
+  const int qi = qt * BM + wave * 32 + li;
+  const int ntiles = p.tile_start[p.n_seg];
+
+  // ---- Q^T fragments, resident for the whole key loop ----
+  bf16x8_t qf[QS];
+  {
+    const bool ok = qi < p.Lq;
+    const uint16_t* qp = p.q + b * p.q_bs + (int64_t)(ok ? qi : 0) * p.q_ls + h * p.q_hs + hg * 8;
+#pragma unroll
+    for (int s = 0; s < QS; ++s) {
+      uint4 v = ok ? *reinterpret_cast<const uint4*>(qp + s * 16) : make_uint4(0, 0, 0, 0);
+      qf[s] = __builtin_bit_cast(bf16x8_t, v);
+    }
+  }
+
+  const int64_t kv_off = b * p.kv_bs + h * p.kv_hs;
+  // rows this thread moves in every tile, as loop-invariant byte offsets from
+  // the tile's first row (buffer loads return 0 past the tile's valid rows)
+  const int kc = tid % NKC;
+  const int kr0 = tid / NKC;
+  const int vkg = tid % 16, vdc = tid / 16;
+  const bool vthread = tid < NVP;
+  constexpr int ESZ = FP8 ? 1 : 2;
+  const int row_bytes = (int)(p.kv_ls * ESZ);
+  int koff[K_LOADS], voff[4];
+#pragma unroll
+  for (int i = 0; i < K_LOADS; ++i) koff[i] = (kr0 + i * KROWS_PER_PASS) * row_bytes + kc * 8 * ESZ;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) voff[e] = (vkg * 4 + e) * row_bytes + vdc * 8 * ESZ;
+
+  // ---- global -> register prefetch of one K/V tile ----
+  raw_t kreg[K_LOADS];
+  raw_t vreg[4];
+  float mreg = 0.0f;
+  TileIter ld;
+  ld.enter(p, 0);
+  auto load_tile = [&]() {
+    const int64_t base = (kv_off + ld.row0 * p.kv_ls) * ESZ;
+    const int nbytes = ld.nvalid() * row_bytes;
+    const auto kr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(reinterpret_cast<const char*>(ld.k) + base), (short)0, nbytes, 0x00020000);
+    const auto vr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(reinterpret_cast<const char*>(ld.v) + base), (short)0, nbytes, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < K_LOADS; ++i) kreg[i] = Chunk::bload(kr, koff[i]);
+    if (vthread) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) vreg[e] = Chunk::bload(vr, voff[e]);
+    }
+    if constexpr (MASK) {
+      if (tid < BN) mreg = tid < ld.nvalid() ? p.mask[b * p.mask_bs + ld.key0 + tid] : 0.0f;
+    }
+    ld.next(p);
+  };
+
+  // ---- register -> LDS store (K rows permuted, V transposed) ----
+  auto store_tile = [&](int buf) {
+    uint16_t* ks = smem + buf * (KBUF + VBUF);
+    uint16_t* vs = ks + KBUF;
+#pragma unroll
+    for (int i = 0; i < K_LOADS; ++i) {
+      const int r = kr0 + i * KROWS_PER_PASS;
+      *reinterpret_cast<uint4*>(ks + sig(r) * KS + kc * 8) = Chunk::to_bf16(kreg[i]);
+    }
+    if (vthread) {
+      uint4 v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = Chunk::to_bf16(vreg[e]);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t a0 = (&v[0].x)[w], a1 = (&v[1].x)[w], a2 = (&v[2].x)[w], a3 = (&v[3].x)[w];
+        // d = vdc*8 + 2w (low halves) and 2w+1 (high halves); keys vkg*4 .. +3
+        uint2 lo, hi;
+        lo.x = __builtin_amdgcn_perm(a1, a0, 0x05040100u);
+        lo.y = __builtin_amdgcn_perm(a3, a2, 0x05040100u);
+        hi.x = __builtin_amdgcn_perm(a1, a0, 0x07060302u);
+        hi.y = __builtin_amdgcn_perm(a3, a2, 0x07060302u);
+        *reinterpret_cast<uint2*>(vs + (vdc * 8 + 2 * w) * VS + vkg * 4) = lo;
+        *reinterpret_cast<uint2*>(vs + (vdc * 8 + 2 * w + 1) * VS + vkg * 4) = hi;
+      }
+    }
+    if constexpr (MASK) {
+      if (tid < BN) mask_s[buf][tid] = mreg;
+    }
+  };
+
+  f32x16_t oacc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) oacc[d] = f32x16_t{};
+  // Running max in the base-2 logit domain.  It is only raised when a new
+  // maximum exceeds it by more than kLazy (then O and l are rescaled); in
+  // between, P = 2^(x - m) may reach 2^kLazy, which float32 sums and bf16 P
+  // represent exactly enough.  Exact: O and l always share the same m.
+  constexpr float kLazy = 8.0f;
+  float m_run = -INFINITY;
+  float l_run = 0.0f;  // sum over this lane's 16-key halves
+
+  if (ntiles > 0) {
+    load_tile();
+    store_tile(0);
+    if (ntiles > 1) load_tile();
+    __syncthreads();
+  }
+  TileIter cp;
+  cp.enter(p, 0);
+
+  for (int j = 0; j < ntiles; ++j) {
+    const int buf = j & 1;
+    if (j + 1 < ntiles) {
+      store_tile(buf ^ 1);
+      if (j + 2 < ntiles) load_tile();
+    }
+    const uint16_t* ks = smem + buf * (KBUF + VBUF);
+    const uint16_t* vs = ks + KBUF;
+    const int nvalid = cp.nvalid();
+
+    // per-tile logit scale (and V scale for fp8)
+    float c_log2 = p.scale_log2;
+    float v_scale = 1.0f;
+    if constexpr (FP8) {
+      const int64_t f = cp.row0 / p.frame;
+      c_log2 *= p.k_sc[cp.s][b * p.sc_bs + h * p.sc_hs + f];
+      v_scale = p.v_sc[cp.s][b * p.sc_bs + h * p.sc_hs + f];
+    }
+
+    // ---- S^T = K Q^T, fragments read one k-step ahead ----
+    f32x16_t sacc[2] = {f32x16_t{}, f32x16_t{}};
+    const uint16_t* kfrag = ks + li * KS + hg * 8;
+    bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(kfrag);
+    bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(kfrag + 32 * KS);
+#pragma unroll
+    for (int s = 0; s < QS; ++s) {
+      bf16x8_t n0 = a0, n1 = a1;
+      if (s + 1 < QS) {
+        n0 = *reinterpret_cast<const bf16x8_t*>(kfrag + (s + 1) * 16);
+        n1 = *reinterpret_cast<const bf16x8_t*>(kfrag + 32 * KS + (s + 1) * 16);
+      }
+      sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[s], sacc[0], 0, 0, 0);
+      sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[s], sacc[1], 0, 0, 0);
+      a0 = n0;
+      a1 = n1;
+    }
+    // first V^T fragments, in flight during the softmax
+    const uint16_t* vfrag = vs + li * VS + hg * 8;
+    bf16x8_t va = *reinterpret_cast<const bf16x8_t*>(vfrag);
+    bf16x8_t vb = *reinterpret_cast<const bf16x8_t*>(vfrag + 16);
+
+    // ---- online softmax on the accumulators (base-2 domain) ----
+    if constexpr (MASK) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb * 32 + 16 * (r >> 3) + 8 * hg + (r & 7);
+          sacc[kb][r] = fmaxf((sacc[kb][r] * p.scale + mask_s[buf][key]) * kLog2e, -3.0e38f);
+        }
+    }
+    if (nvalid < BN) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb * 32 + 16 * (r >> 3) + 8 * hg + (r & 7);
+          if (key >= nvalid) sacc[kb][r] = -INFINITY;
+        }
+    }
+    float mt = sacc[0][0];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[kb][r]);
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    // logits are x = s * c (c > 0), so max(x) = max(s) * c
+    const float c = MASK ? 1.0f : c_log2;
+    const float m_tile = mt * c;
+    const bool raise = m_tile > m_run + kLazy;
+    if (__builtin_amdgcn_ballot_w64(raise)) {
+      const float m_new = fmaxf(m_run, m_tile);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
+    }
+    // all keys masked so far: keep the exponent finite
+    const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
+
+    float psum = 0.0f;
+    bf16x8_t pf[4];
+#pragma unroll
+    for (int ks4 = 0; ks4 < 4; ++ks4) {
+      const int kb = ks4 >> 1, t = ks4 & 1;
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][8 * t + e], c, -m_use));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][8 * t + e + 1], c, -m_use));
+        psum += p0 + p1;
+        w[e >> 1] = FP8 ? pack_bf16x2(p0 * v_scale, p1 * v_scale) : pack_bf16x2(p0, p1);
+      }
+      pf[ks4] = __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
+    }
+    l_run += psum;
+
+    // ---- O^T += V^T P^T, fragments read one step ahead ----
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+#pragma unroll
+      for (int ks4 = 0; ks4 < 4; ks4 += 2) {
+        bf16x8_t na = va, nb = vb;
+        const int nd = (ks4 + 2 < 4) ? d : d + 1;
+        const int nk = (ks4 + 2 < 4) ? ks4 + 2 : 0;
+        if (nd < DB) {
+          na = *reinterpret_cast<const bf16x8_t*>(vfrag + nd * 32 * VS + nk * 16);
+          nb = *reinterpret_cast<const bf16x8_t*>(vfrag + nd * 32 * VS + (nk + 1) * 16);
+        }
+        oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pf[ks4], oacc[d], 0, 0, 0);
+        oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb, pf[ks4 + 1], oacc[d], 0, 0, 0);
+        va = na;
+        vb = nb;
+      }
+    }
+    cp.next(p);
+    __syncthreads();
+  }
+
+  // ---- epilogue: combine the two lane halves' sums, normalise, store ----
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  if (qi < p.Lq) {
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    uint16_t* op = p.o + b * p.o_bs + (int64_t)qi * p.o_ls + h * p.o_hs;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        uint2 w;
+        w.x = pack_bf16x2(oacc[d][4 * g4] * inv, oacc[d][4 * g4 + 1] * inv);
+        w.y = pack_bf16x2(oacc[d][4 * g4 + 2] * inv, oacc[d][4 * g4 + 3] * inv);
+        *reinterpret_cast<uint2*>(op + d * 32 + 8 * g4 + 4 * hg) = w;
+      }
+    }
+    if (p.lse != nullptr && hg == 0) {
+      const float lse2 = m_run + __log2f(l_tot);
+      p.lse[((int64_t)b * p.H + h) * p.Lq + qi] = lse2 / kLog2e;
+    }
+  }
+}
+
+template <int D, bool FP8, bool MASK>
+int launch_flash(const FlashParams& p, hipStream_t st) {
+  const int64_t nblocks = (int64_t)p.B * p.H * p.n_qtiles;
+  LTX_REQUIRE(nblocks <= 0x7FFFFFFF, "ltx_flash_attn_fwd: grid too large");
+  hipLaunchKernelGGL((flash_fwd_kernel<D, FP8, MASK>), dim3((unsigned)nblocks), dim3(256), 0, st, p);
+  LTX_LAUNCH_CHECK("ltx_flash_attn_fwd");
+  return LTX_OK;
+}
+
+}  // namespace ltx
+
+using namespace ltx;
+
+extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t H, int64_t D,
+                                  int64_t q_bs, int64_t q_ls, int64_t q_hs, int64_t n_segments,
+                                  const void* const* k_ptrs, const void* const* v_ptrs,
+                                  const int64_t* seg_lens, int64_t kv_bs, int64_t kv_ls,
+                                  int64_t kv_hs, int kv_dtype, const float* const* k_scales,
+                                  const float* const* v_scales, int64_t sc_bs, int64_t sc_hs,
+                                  int64_t frame_tokens, const float* key_mask, int64_t mask_bs,
+                                  void* out, int64_t o_bs, int64_t o_ls, int64_t o_hs, float* lse,
+                                  float scale, void* stream) {
+  clear_error();
+  LTX_REQUIRE(q && out, "ltx_flash_attn_fwd: null q/out");
+  LTX_REQUIRE(D == 64 || D == 128, "ltx_flash_attn_fwd: head dim %lld unsupported (64 or 128)",
+              (long long)D);
+  LTX_REQUIRE(B >= 1 && H >= 1 && Lq >= 0 && Lq <= 0x7FFFFFFF, "ltx_flash_attn_fwd: bad B/H/Lq");
+  LTX_REQUIRE(n_segments >= 0 && n_segments <= LTX_MAX_SEGMENTS,
+              "ltx_flash_attn_fwd: n_segments must be in [0, %d]", LTX_MAX_SEGMENTS);
+  LTX_REQUIRE(kv_dtype == LTX_BF16 || kv_dtype == LTX_F8E4M3, "ltx_flash_attn_fwd: kv_dtype must be BF16 or F8E4M3");
+  LTX_REQUIRE(n_segments == 0 || (k_ptrs && v_ptrs && seg_lens), "ltx_flash_attn_fwd: null segment arrays");
+  const bool fp8 = kv_dtype == LTX_F8E4M3;
+  const int64_t esz = fp8 ? 1 : 2;
+  auto al = [](const void* ptr, uintptr_t a) { return ((uintptr_t)ptr % a) == 0; };
+  LTX_REQUIRE(al(q, 16) && (q_bs * 2) % 16 == 0 && (q_ls * 2) % 16 == 0 && (q_hs * 2) % 16 == 0,
+              "ltx_flash_attn_fwd: q rows must be 16-byte aligned");
+  LTX_REQUIRE(al(out, 8) && (o_bs * 2) % 8 == 0 && (o_ls * 2) % 8 == 0 && (o_hs * 2) % 8 == 0,
+              "ltx_flash_attn_fwd: out rows must be 8-byte aligned");
+  LTX_REQUIRE((kv_bs * esz) % 16 == 0 && (kv_ls * esz) % 16 == 0 && (kv_hs * esz) % 16 == 0,
+              "ltx_flash_attn_fwd: kv strides must keep 16-byte rows");
+
+  FlashParams p{};
+  p.q = (const uint16_t*)q;
+  p.o = (uint16_t*)out;
+  p.lse = lse;
+  p.mask = key_mask;
+  p.q_bs = q_bs; p.q_ls = q_ls; p.q_hs = q_hs;
+  p.o_bs = o_bs; p.o_ls = o_ls; p.o_hs = o_hs;
+  p.kv_bs = kv_bs; p.kv_ls = kv_ls; p.kv_hs = kv_hs;
+  p.sc_bs = sc_bs; p.sc_hs = sc_hs;
+  p.mask_bs = mask_bs;
+  p.B = (int)B; p.H = (int)H; p.Lq = (int)Lq;
+  p.frame = (int)(frame_tokens > 0 ? frame_tokens : 1);
+  p.scale = scale > 0.0f ? scale : 1.0f / sqrtf((float)D);
+  p.scale_log2 = p.scale * kLog2e;
+  // drop empty segments
+  int n = 0;
+  p.seg_start[0] = 0;
+  for (int64_t i = 0; i < n_segments; ++i) {
+    LTX_REQUIRE(seg_lens[i] >= 0, "ltx_flash_attn_fwd: negative segment length");
+    if (seg_lens[i] == 0) continue;
+    LTX_REQUIRE(k_ptrs[i] && v_ptrs[i], "ltx_flash_attn_fwd: null segment %lld", (long long)i);
+    LTX_REQUIRE(al(k_ptrs[i], 16) && al(v_ptrs[i], 16), "ltx_flash_attn_fwd: segment %lld not 16-byte aligned",
+                (long long)i);
+    if (fp8) {
+      LTX_REQUIRE(k_scales && v_scales && k_scales[i] && v_scales[i],
+                  "ltx_flash_attn_fwd: fp8 segment %lld needs k/v scales", (long long)i);
+      LTX_REQUIRE(frame_tokens > 0 && frame_tokens % kBN == 0,
+                  "ltx_flash_attn_fwd: fp8 needs frame_tokens to be a multiple of %d (got %lld)", kBN,
+                  (long long)frame_tokens);
+      p.k_sc[n] = k_scales[i];
+      p.v_sc[n] = v_scales[i];
+    }
+    p.k_ptr[n] = k_ptrs[i];
+    p.v_ptr[n] = v_ptrs[i];
+    p.seg_start[n + 1] = p.seg_start[n] + seg_lens[i];
+    const int64_t tiles = p.tile_start[n] + (seg_lens[i] + kBN - 1) / kBN;
+    LTX_REQUIRE(tiles <= 0x7FFFFFFF, "ltx_flash_attn_fwd: too many keys");
+    p.tile_start[n + 1] = (int)tiles;
+    ++n;
+  }
+  p.n_seg = n;
+  p.Lk = p.seg_start[n];
+  if (key_mask) LTX_REQUIRE(!fp8, "ltx_flash_attn_fwd: key mask with fp8 KV is not built");
+  LTX_REQUIRE(kv_ls * esz * kBN < (int64_t)1 << 31 && kv_ls >= D,
+              "ltx_flash_attn_fwd: kv token stride %lld out of range", (long long)kv_ls);
+  p.n_qtiles = (int)((Lq + kBM - 1) / kBM);
+  if (Lq == 0) return LTX_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (n == 0) {
+    // no keys: softmax over an empty set; SDPA returns NaN rows, we define zeros
+    LTX_REQUIRE(false, "ltx_flash_attn_fwd: no keys (Lk == 0)");
+  }
+  if (D == 128) {
+    if (fp8) return launch_flash<128, true, false>(p, st);
+    if (key_mask) return launch_flash<128, false, true>(p, st);
+    return launch_flash<128, false, false>(p, st);
+  } else {
+    if (fp8) return launch_flash<64, true, false>(p, st);
+    if (key_mask) return launch_flash<64, false, true>(p, st);
+    return launch_flash<64, false, false>(p, st);
+  }
+}

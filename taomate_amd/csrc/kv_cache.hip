@@ -1,0 +1,239 @@
+// KV-cache append (copy or fp8-e4m3 quantise) and span gather (compaction).
+//
+// The reference appends with torch.cat, reallocating and copying the whole cache
+// on every commit (ltx_causal/transformer/kv_cache.py:394-398, :2642-2656), and
+// evicts by slicing and re-concatenating segment spans (taomate/inference/
+// cache.py:28-67).  Here the cache is a preallocated arena: append writes only
+// the new tokens into their slots, eviction is slot bookkeeping on the host,
+// and gather is the optional physical compaction of the surviving spans.
+
+#include "ltx_common.h"
+
+namespace ltx {
+
+// One thread moves one 16-byte chunk of a (b, l, h) row.
+template <typename TS>
+__global__ void kv_copy_kernel(const TS* __restrict__ src, int64_t s_bs, int64_t s_ls, int64_t s_hs,
+                               uint16_t* __restrict__ dst, int64_t d_bs, int64_t d_ls, int64_t d_hs,
+                               int64_t L, int H, int D) {
+  const int cpr = D / 8;  // 8 elements per chunk
+  const int64_t total = (int64_t)gridDim.y * L * H * cpr;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= L * H * cpr) return;
+  (void)total;
+  const int b = blockIdx.y;
+  const int c = (int)(gid % cpr);
+  const int64_t lh = gid / cpr;
+  const int h = (int)(lh % H);
+  const int64_t l = lh / H;
+  const TS* s = src + b * s_bs + l * s_ls + h * s_hs + c * 8;
+  uint16_t* d = dst + b * d_bs + l * d_ls + h * d_hs + c * 8;
+  if constexpr (sizeof(TS) == 2) {
+    *reinterpret_cast<uint4*>(d) = *reinterpret_cast<const uint4*>(s);
+  } else {
+    float4 a = reinterpret_cast<const float4*>(s)[0];
+    float4 bb = reinterpret_cast<const float4*>(s)[1];
+    uint4 o;
+    o.x = pack_bf16x2(a.x, a.y);
+    o.y = pack_bf16x2(a.z, a.w);
+    o.z = pack_bf16x2(bb.x, bb.y);
+    o.w = pack_bf16x2(bb.z, bb.w);
+    *reinterpret_cast<uint4*>(d) = o;
+  }
+}
+
+// One workgroup per (frame, h, b): absmax over frame_tokens x D, then quantise.
+template <typename TS>
+__global__ void __launch_bounds__(256) kv_quant_kernel(
+    const TS* __restrict__ src, int64_t s_bs, int64_t s_ls, int64_t s_hs, uint8_t* __restrict__ dst,
+    int64_t d_bs, int64_t d_ls, int64_t d_hs, float* __restrict__ scales, int64_t sc_bs,
+    int64_t sc_hs, int frame_tokens, int D) {
+  const int f = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int cpr = D / 8;
+  const int n = frame_tokens * cpr;  // 8-element chunks in this (frame, head)
+  const int64_t l0 = (int64_t)f * frame_tokens;
+  const TS* sbase = src + b * s_bs + l0 * s_ls + h * s_hs;
+  uint8_t* dbase = dst + b * d_bs + l0 * d_ls + h * d_hs;
+
+  auto load8 = [&](int idx, float* v) {
+    const int t = idx / cpr, c = idx % cpr;
+    const TS* p = sbase + (int64_t)t * s_ls + c * 8;
+    if constexpr (sizeof(TS) == 2) {
+      uint4 r = *reinterpret_cast<const uint4*>(p);
+      const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = bf16_bits_to_f32(w[i] & 0xFFFFu);
+        v[2 * i + 1] = bf16_bits_to_f32(w[i] >> 16);
+      }
+    } else {
+      float4 a = reinterpret_cast<const float4*>(p)[0];
+      float4 bb = reinterpret_cast<const float4*>(p)[1];
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+      v[4] = bb.x; v[5] = bb.y; v[6] = bb.z; v[7] = bb.w;
+    }
+  };
+
+  float amax = 0.0f;
+  for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
+    float v[8];
+    load8(idx, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  __shared__ float red[4];
+  __shared__ float scale_s;
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float sc = m > 0.0f ? __fdiv_rn(m, 448.0f) : 1.0f;
+    scale_s = sc;
+    scales[b * sc_bs + h * sc_hs + f] = sc;
+  }
+  __syncthreads();
+  const float sc = scale_s;
+  for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
+    float v[8];
+    load8(idx, v);
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lo |= f32_to_e4m3(__fdiv_rn(v[i], sc)) << (8 * i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hi |= f32_to_e4m3(__fdiv_rn(v[4 + i], sc)) << (8 * i);
+    const int t = idx / cpr, c = idx % cpr;
+    *reinterpret_cast<uint2*>(dbase + (int64_t)t * d_ls + c * 8) = make_uint2(lo, hi);
+  }
+}
+
+struct SpanTable {
+  int64_t src_start[LTX_MAX_SEGMENTS];
+  int64_t dst_start[LTX_MAX_SEGMENTS + 1];
+  int n;
+};
+
+// One thread per 4-byte word of a destination (b, l, h) row.
+__global__ void kv_gather_kernel(const uint32_t* __restrict__ src, int64_t s_bs, int64_t s_ls,
+                                 int64_t s_hs, uint32_t* __restrict__ dst, int64_t d_bs,
+                                 int64_t d_ls, int64_t d_hs, SpanTable spans, int H, int wpr) {
+  const int64_t Ltot = spans.dst_start[spans.n];
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= Ltot * H * wpr) return;
+  const int b = blockIdx.y;
+  const int w = (int)(gid % wpr);
+  const int64_t lh = gid / wpr;
+  const int h = (int)(lh % H);
+  const int64_t l = lh / H;
+  int s = 0;
+#pragma unroll
+  for (int i = 1; i < LTX_MAX_SEGMENTS; ++i)
+    if (i < spans.n && l >= spans.dst_start[i]) s = i;
+  const int64_t sl = spans.src_start[s] + (l - spans.dst_start[s]);
+  dst[b * d_bs + l * d_ls + h * d_hs + w] = src[b * s_bs + sl * s_ls + h * s_hs + w];
+}
+
+}  // namespace ltx
+
+using namespace ltx;
+
+extern "C" int ltx_kv_append(int src_dtype, int dst_dtype, int64_t B, int64_t L, int64_t H,
+                             int64_t D, const void* src, int64_t s_bs, int64_t s_ls, int64_t s_hs,
+                             void* dst, int64_t d_bs, int64_t d_ls, int64_t d_hs, float* scales,
+                             int64_t sc_bs, int64_t sc_hs, int64_t frame_tokens, void* stream) {
+  clear_error();
+  LTX_REQUIRE(src_dtype == LTX_BF16 || src_dtype == LTX_F32, "ltx_kv_append: src_dtype must be BF16 or F32");
+  LTX_REQUIRE(dst_dtype == LTX_BF16 || dst_dtype == LTX_F8E4M3,
+              "ltx_kv_append: dst_dtype must be BF16 or F8E4M3");
+  LTX_REQUIRE(B >= 1 && B <= 65535 && L >= 0 && H >= 1 && D >= 8 && D % 8 == 0,
+              "ltx_kv_append: bad shape");
+  LTX_REQUIRE(src && dst, "ltx_kv_append: null pointer");
+  const int64_t ssz = src_dtype == LTX_BF16 ? 2 : 4;
+  const int64_t dsz = dst_dtype == LTX_BF16 ? 2 : 1;
+  LTX_REQUIRE(((uintptr_t)src % 16) == 0 && (s_bs * ssz) % 16 == 0 && (s_ls * ssz) % 16 == 0 &&
+                  (s_hs * ssz) % 16 == 0,
+              "ltx_kv_append: src must be 16-byte aligned per row");
+  LTX_REQUIRE(((uintptr_t)dst % 8) == 0 && (d_bs * dsz) % 8 == 0 && (d_ls * dsz) % 8 == 0 &&
+                  (d_hs * dsz) % 8 == 0,
+              "ltx_kv_append: dst must be 8-byte aligned per row");
+  if (L == 0) return LTX_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (dst_dtype == LTX_BF16) {
+    LTX_REQUIRE(((uintptr_t)dst % 16) == 0 && (d_bs * 2) % 16 == 0 && (d_ls * 2) % 16 == 0 &&
+                    (d_hs * 2) % 16 == 0,
+                "ltx_kv_append: bf16 dst must be 16-byte aligned per row");
+    const int64_t n = L * H * (D / 8);
+    const dim3 grid((unsigned)ceil_div(n, 256), (unsigned)B);
+    if (src_dtype == LTX_BF16)
+      hipLaunchKernelGGL(kv_copy_kernel<uint16_t>, grid, dim3(256), 0, st, (const uint16_t*)src, s_bs,
+                         s_ls, s_hs, (uint16_t*)dst, d_bs, d_ls, d_hs, L, (int)H, (int)D);
+    else
+      hipLaunchKernelGGL(kv_copy_kernel<float>, grid, dim3(256), 0, st, (const float*)src, s_bs, s_ls,
+                         s_hs, (uint16_t*)dst, d_bs, d_ls, d_hs, L, (int)H, (int)D);
+  } else {
+    LTX_REQUIRE(scales != nullptr, "ltx_kv_append: fp8 needs a scales buffer");
+    LTX_REQUIRE(frame_tokens >= 1 && L % frame_tokens == 0,
+                "ltx_kv_append: L (%lld) must be a multiple of frame_tokens (%lld)", (long long)L,
+                (long long)frame_tokens);
+    const dim3 grid((unsigned)(L / frame_tokens), (unsigned)H, (unsigned)B);
+    if (src_dtype == LTX_BF16)
+      hipLaunchKernelGGL(kv_quant_kernel<uint16_t>, grid, dim3(256), 0, st, (const uint16_t*)src, s_bs,
+                         s_ls, s_hs, (uint8_t*)dst, d_bs, d_ls, d_hs, scales, sc_bs, sc_hs,
+                         (int)frame_tokens, (int)D);
+    else
+      hipLaunchKernelGGL(kv_quant_kernel<float>, grid, dim3(256), 0, st, (const float*)src, s_bs, s_ls,
+                         s_hs, (uint8_t*)dst, d_bs, d_ls, d_hs, scales, sc_bs, sc_hs,
+                         (int)frame_tokens, (int)D);
+  }
+  LTX_LAUNCH_CHECK("ltx_kv_append");
+  return LTX_OK;
+}
+
+extern "C" int ltx_kv_gather(int64_t elem_bytes, int64_t B, int64_t H, int64_t D, const void* src,
+                             int64_t s_bs, int64_t s_ls, int64_t s_hs, void* dst, int64_t d_bs,
+                             int64_t d_ls, int64_t d_hs, int64_t n_spans, const int64_t* starts,
+                             const int64_t* lens, void* stream) {
+  clear_error();
+  LTX_REQUIRE(elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4, "ltx_kv_gather: elem_bytes must be 1, 2 or 4");
+  LTX_REQUIRE(B >= 1 && B <= 65535 && H >= 1 && D >= 1 && (D * elem_bytes) % 4 == 0,
+              "ltx_kv_gather: D*elem_bytes must be a multiple of 4");
+  LTX_REQUIRE(n_spans >= 0 && n_spans <= LTX_MAX_SEGMENTS, "ltx_kv_gather: at most %d spans",
+              LTX_MAX_SEGMENTS);
+  LTX_REQUIRE(src && dst && (n_spans == 0 || (starts && lens)), "ltx_kv_gather: null pointer");
+  LTX_REQUIRE(((uintptr_t)src % 4) == 0 && ((uintptr_t)dst % 4) == 0 && (s_bs * elem_bytes) % 4 == 0 &&
+                  (s_ls * elem_bytes) % 4 == 0 && (s_hs * elem_bytes) % 4 == 0 &&
+                  (d_bs * elem_bytes) % 4 == 0 && (d_ls * elem_bytes) % 4 == 0 &&
+                  (d_hs * elem_bytes) % 4 == 0,
+              "ltx_kv_gather: rows must be 4-byte aligned");
+  SpanTable t{};
+  t.n = (int)n_spans;
+  t.dst_start[0] = 0;
+  for (int i = 0; i < n_spans; ++i) {
+    LTX_REQUIRE(starts[i] >= 0 && lens[i] >= 0, "ltx_kv_gather: negative span");
+    t.src_start[i] = starts[i];
+    t.dst_start[i + 1] = t.dst_start[i] + lens[i];
+  }
+  const int64_t Ltot = t.dst_start[n_spans];
+  if (Ltot == 0) return LTX_OK;
+  if (t.n == 0) return LTX_OK;
+  // drop empty spans so every span in the table owns at least one token
+  SpanTable c{};
+  c.dst_start[0] = 0;
+  for (int i = 0; i < t.n; ++i) {
+    const int64_t len = t.dst_start[i + 1] - t.dst_start[i];
+    if (len == 0) continue;
+    c.src_start[c.n] = t.src_start[i];
+    c.dst_start[c.n + 1] = c.dst_start[c.n] + len;
+    c.n++;
+  }
+  const int wpr = (int)(D * elem_bytes / 4);
+  const int64_t w = 4 / elem_bytes;  // elements per word
+  const int64_t n = Ltot * H * wpr;
+  const dim3 grid((unsigned)ceil_div(n, 256), (unsigned)B);
+  hipLaunchKernelGGL(kv_gather_kernel, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                     (const uint32_t*)src, s_bs / w, s_ls / w, s_hs / w, (uint32_t*)dst, d_bs / w,
+                     d_ls / w, d_hs / w, c, (int)H, wpr);
+  LTX_LAUNCH_CHECK("ltx_kv_gather");
+  return LTX_OK;
+}

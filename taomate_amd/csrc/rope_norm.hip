@@ -1,0 +1,366 @@
+// RoPE tables and the fused full-row QK-RMSNorm + SPLIT RoPE kernel (gfx950).
+//
+// Both kernels are HBM-bound streams: one workgroup owns one token row, loads
+// it once with 16-byte vector loads, reduces its sum of squares across the
+// workgroup, and writes the normalised, rotated row once.
+
+#include "ltx_common.h"
+
+namespace ltx {
+
+// ---------------------------------------------------------------------------
+// RoPE table (causal_rope.py:139-357, SPLIT branch).
+// One thread per (token, global pair index); output [B, H, T, P], P = dim/(2H).
+// All position arithmetic is float32 with explicit IEEE ops (no contraction) so
+// the angles equal what the reference's float32 tensor ops produce.
+// ---------------------------------------------------------------------------
+template <typename TOut>
+__global__ void rope_table_kernel(TOut* __restrict__ cos_out, TOut* __restrict__ sin_out,
+                                  const float* __restrict__ freq_idx, int n_freq,
+                                  int num_pos_dims, int grid_h, int grid_w,
+                                  int64_t start_frame, int is_audio, float max_t,
+                                  float max_h, float max_w, int half_dim, int heads,
+                                  int64_t T, int batch) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= T * half_dim) return;
+  const int64_t t = gid / half_dim;
+  const int g = (int)(gid % half_dim);  // global pair index within the token
+  const int pad = half_dim - n_freq * num_pos_dims;
+  float c = 1.0f, s = 0.0f;
+  if (g >= pad) {
+    const int q = g - pad;
+    const int fi = q / num_pos_dims;
+    const int axis = q % num_pos_dims;
+    float frac;
+    if (num_pos_dims == 3) {
+      const int64_t hw = (int64_t)grid_h * grid_w;
+      const int64_t f = t / hw;
+      const int64_t rem = t % hw;
+      if (axis == 0) {
+        // latent frame -> pixel-frame bounds with the causal fix -> seconds
+        // (causal_rope.py:264-267), then / max_pos[0] (:275)
+        float lt = (float)(start_frame + f);
+        float ps = fmaxf(__fadd_rn(__fadd_rn(__fmul_rn(lt, 8.0f), 1.0f), -8.0f), 0.0f);
+        float pe = fmaxf(
+            __fadd_rn(__fadd_rn(__fmul_rn(__fadd_rn(lt, 1.0f), 8.0f), 1.0f), -8.0f), 0.0f);
+        float sec = __fdiv_rn(__fdiv_rn(__fadd_rn(ps, pe), 2.0f), 24.0f);
+        frac = __fdiv_rn(sec, max_t);
+      } else {
+        // spatial pixel midpoints (causal_rope.py:271-277)
+        int64_t idx = (axis == 1) ? (rem / grid_w) : (rem % grid_w);
+        float px = __fadd_rn(__fmul_rn((float)idx, 32.0f), 16.0f);
+        frac = __fdiv_rn(px, axis == 1 ? max_h : max_w);
+      }
+    } else {
+      float lt = (float)(start_frame + t);
+      float sec;
+      if (is_audio) {
+        // mel-frame bounds -> seconds (causal_rope.py:298-300)
+        float ms = fmaxf(__fadd_rn(__fadd_rn(__fmul_rn(lt, 4.0f), 1.0f), -4.0f), 0.0f);
+        float me = fmaxf(
+            __fadd_rn(__fadd_rn(__fmul_rn(__fadd_rn(lt, 1.0f), 4.0f), 1.0f), -4.0f), 0.0f);
+        sec = __fdiv_rn(__fmul_rn(__fdiv_rn(__fadd_rn(ms, me), 2.0f), 160.0f), 16000.0f);
+      } else {
+        float ps = fmaxf(__fadd_rn(__fadd_rn(__fmul_rn(lt, 8.0f), 1.0f), -8.0f), 0.0f);
+        float pe = fmaxf(
+            __fadd_rn(__fadd_rn(__fmul_rn(__fadd_rn(lt, 1.0f), 8.0f), 1.0f), -8.0f), 0.0f);
+        sec = __fdiv_rn(__fdiv_rn(__fadd_rn(ps, pe), 2.0f), 24.0f);
+      }
+      frac = __fdiv_rn(sec, max_t);
+    }
+    // freqs = indices * (frac * 2 - 1)   (causal_rope.py:287)
+    float ang = __fmul_rn(freq_idx[fi], __fadd_rn(__fmul_rn(frac, 2.0f), -1.0f));
+    c = cosf(ang);
+    s = sinf(ang);
+  }
+  const int per_head = half_dim / heads;
+  const int h = g / per_head;
+  const int j = g % per_head;
+  for (int b = 0; b < batch; ++b) {
+    int64_t o = (((int64_t)b * heads + h) * T + t) * per_head + j;
+    if constexpr (sizeof(TOut) == 2) {
+      cos_out[o] = f32_to_bf16_bits(c);
+      sin_out[o] = f32_to_bf16_bits(s);
+    } else {
+      cos_out[o] = c;
+      sin_out[o] = s;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fused RMSNorm + SPLIT RoPE.  Block = (H*D)/16 threads; thread (h, c) owns the
+// 8 elements [c*8, c*8+8) of head h's first half and the matching 8 of its
+// second half, i.e. the 8 (x1, x2) rotation pairs j = c*8 .. c*8+7.
+// grid = (rows, B, 2): z selects q (0) or k (1).
+// ---------------------------------------------------------------------------
+struct NormRopeSide {
+  const void* in;
+  void* out;
+  const void* gamma;
+  const void* cos;
+  const void* sin;
+  int64_t len, in_bs, in_ls, out_bs, out_ls, tb, th, tt;
+  float eps;
+};
+
+template <typename T>
+struct Vec8;
+template <>
+struct Vec8<uint16_t> {
+  uint4 raw;
+  __device__ __forceinline__ void load(const uint16_t* p) {
+    raw = *reinterpret_cast<const uint4*>(p);
+  }
+  __device__ __forceinline__ void store(uint16_t* p) const {
+    *reinterpret_cast<uint4*>(p) = raw;
+  }
+  __device__ __forceinline__ float get(int i) const {
+    uint32_t w = (&raw.x)[i >> 1];
+    return bf16_bits_to_f32((i & 1) ? (w >> 16) : (w & 0xFFFFu));
+  }
+  __device__ __forceinline__ void set(int i, float v) {
+    uint32_t& w = (&raw.x)[i >> 1];
+    uint32_t b = f32_to_bf16_bits(v);
+    w = (i & 1) ? ((w & 0xFFFFu) | (b << 16)) : ((w & 0xFFFF0000u) | b);
+  }
+};
+template <>
+struct Vec8<float> {
+  float4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = reinterpret_cast<const float4*>(p)[0];
+    b = reinterpret_cast<const float4*>(p)[1];
+  }
+  __device__ __forceinline__ void store(float* p) const {
+    reinterpret_cast<float4*>(p)[0] = a;
+    reinterpret_cast<float4*>(p)[1] = b;
+  }
+  __device__ __forceinline__ float get(int i) const {
+    return i < 4 ? (&a.x)[i] : (&b.x)[i - 4];
+  }
+  __device__ __forceinline__ void set(int i, float v) {
+    if (i < 4) (&a.x)[i] = v; else (&b.x)[i - 4] = v;
+  }
+};
+
+// Round a float32 intermediate to the storage type (bf16 rounds, f32 keeps).
+template <typename T>
+__device__ __forceinline__ float rnd(float v) {
+  if constexpr (sizeof(T) == 2) return bf16_bits_to_f32(f32_to_bf16_bits(v));
+  else return v;
+}
+
+template <typename T, typename TT>
+__global__ void __launch_bounds__(256) qk_norm_rope_kernel(NormRopeSide qs, NormRopeSide ks,
+                                                           int H, int D) {
+  const NormRopeSide& sd = (blockIdx.z == 0) ? qs : ks;
+  const int64_t row = blockIdx.x;
+  if (row >= sd.len) return;  // uniform across the block
+  const int b = blockIdx.y;
+  const int HD = H * D;
+  const int cpd = D / 16;  // chunks of 8 pairs per head
+  const int tid = threadIdx.x;
+  const int h = tid / cpd;
+  const int c = tid % cpd;
+  const int e1 = h * D + c * 8;
+  const int e2 = e1 + D / 2;
+
+  const T* in = reinterpret_cast<const T*>(sd.in) + b * sd.in_bs + row * sd.in_ls;
+  Vec8<T> x1, x2;
+  x1.load(in + e1);
+  x2.load(in + e2);
+
+  float v1[8], v2[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    v1[i] = x1.get(i);
+    v2[i] = x2.get(i);
+  }
+
+  if (sd.eps >= 0.0f) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += v1[i] * v1[i] + v2[i] * v2[i];
+    // wavefront reduction then across the block's waves through LDS
+    // xor partners stay inside the block (blocks of 16 or 32 threads use part of a wave)
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+      if (off < (int)blockDim.x) ss += __shfl_xor(ss, off, 64);
+    __shared__ float red[16];
+    const int wave = tid >> 6, lane = tid & 63;
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    const int nwaves = (blockDim.x + 63) >> 6;
+    float tot = 0.0f;
+    for (int w = 0; w < nwaves; ++w) tot += red[w];
+    // y = (x * rsqrt(mean(x^2) + eps)) * gamma in float32, rounded once: the
+    // fused rms_norm of PyTorch (bit-identical to torch.nn.functional.rms_norm
+    // on bf16 rows, checked against it by the tests)
+    const float r = 1.0f / sqrtf(__fadd_rn(__fdiv_rn(tot, (float)HD), sd.eps));
+    Vec8<T> g1, g2;
+    const bool has_gamma = sd.gamma != nullptr;
+    if (has_gamma) {
+      g1.load(reinterpret_cast<const T*>(sd.gamma) + e1);
+      g2.load(reinterpret_cast<const T*>(sd.gamma) + e2);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float y1 = __fmul_rn(v1[i], r), y2 = __fmul_rn(v2[i], r);
+      if (has_gamma) {
+        y1 = __fmul_rn(y1, g1.get(i));
+        y2 = __fmul_rn(y2, g2.get(i));
+      }
+      v1[i] = rnd<T>(y1);
+      v2[i] = rnd<T>(y2);
+    }
+  }
+
+  if (sd.cos != nullptr) {
+    const TT* cp = reinterpret_cast<const TT*>(sd.cos) + b * sd.tb + h * sd.th + row * sd.tt + c * 8;
+    const TT* sp = reinterpret_cast<const TT*>(sd.sin) + b * sd.tb + h * sd.th + row * sd.tt + c * 8;
+    Vec8<TT> cv, sv;
+    cv.load(cp);
+    sv.load(sp);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float cc = cv.get(i), s = sv.get(i);
+      // out1 = x1*c ; out1 += (-s)*x2 ; out2 = x2*c ; out2 += s*x1
+      // (causal_rope.py:121-126: one rounding after the multiply, one after
+      // the float32 multiply-add)
+      const float a1 = rnd<T>(__fmul_rn(v1[i], cc));
+      const float a2 = rnd<T>(__fmul_rn(v2[i], cc));
+      const float o1 = rnd<T>(__fadd_rn(a1, __fmul_rn(-s, v2[i])));
+      const float o2 = rnd<T>(__fadd_rn(a2, __fmul_rn(s, v1[i])));
+      v1[i] = o1;
+      v2[i] = o2;
+    }
+  }
+
+  T* out = reinterpret_cast<T*>(sd.out) + b * sd.out_bs + row * sd.out_ls;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    x1.set(i, v1[i]);
+    x2.set(i, v2[i]);
+  }
+  x1.store(out + e1);
+  x2.store(out + e2);
+}
+
+}  // namespace ltx
+
+using namespace ltx;
+
+extern "C" int ltx_rope_table(void* cos_out, void* sin_out, int out_dtype, const float* freq_idx,
+                              int64_t n_freq, int num_pos_dims, int64_t grid_f, int64_t grid_h,
+                              int64_t grid_w, int64_t start_frame, int is_audio, float max_pos_t,
+                              float max_pos_h, float max_pos_w, int64_t dim, int64_t num_heads,
+                              int64_t batch, void* stream) {
+  clear_error();
+  LTX_REQUIRE(cos_out && sin_out && freq_idx, "ltx_rope_table: null pointer");
+  LTX_REQUIRE(num_pos_dims == 1 || num_pos_dims == 3, "ltx_rope_table: num_pos_dims must be 1 or 3");
+  LTX_REQUIRE(out_dtype == LTX_F32 || out_dtype == LTX_BF16, "ltx_rope_table: out_dtype must be F32 or BF16");
+  LTX_REQUIRE(dim > 0 && dim % 2 == 0 && num_heads > 0 && (dim / 2) % num_heads == 0,
+              "ltx_rope_table: dim/2 must be divisible by num_heads");
+  LTX_REQUIRE(n_freq >= 0 && n_freq * num_pos_dims <= dim / 2,
+              "ltx_rope_table: n_freq*num_pos_dims exceeds dim/2");
+  LTX_REQUIRE(grid_f >= 0 && batch >= 1, "ltx_rope_table: bad grid/batch");
+  if (num_pos_dims == 3) LTX_REQUIRE(grid_h > 0 && grid_w > 0, "ltx_rope_table: bad spatial grid");
+  const int64_t T = num_pos_dims == 3 ? grid_f * grid_h * grid_w : grid_f;
+  const int half = (int)(dim / 2);
+  const int64_t n = T * half;
+  if (n == 0) return LTX_OK;
+  const int threads = 256;
+  const dim3 grid((unsigned)ceil_div(n, threads));
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (out_dtype == LTX_BF16) {
+    hipLaunchKernelGGL(rope_table_kernel<uint16_t>, grid, dim3(threads), 0, st,
+                       (uint16_t*)cos_out, (uint16_t*)sin_out, freq_idx, (int)n_freq, num_pos_dims,
+                       (int)grid_h, (int)grid_w, start_frame, is_audio, max_pos_t, max_pos_h,
+                       max_pos_w, half, (int)num_heads, T, (int)batch);
+  } else {
+    hipLaunchKernelGGL(rope_table_kernel<float>, grid, dim3(threads), 0, st, (float*)cos_out,
+                       (float*)sin_out, freq_idx, (int)n_freq, num_pos_dims, (int)grid_h,
+                       (int)grid_w, start_frame, is_audio, max_pos_t, max_pos_h, max_pos_w, half,
+                       (int)num_heads, T, (int)batch);
+  }
+  LTX_LAUNCH_CHECK("ltx_rope_table");
+  return LTX_OK;
+}
+
+extern "C" int ltx_qk_rmsnorm_rope(int dtype, int64_t B, int64_t H, int64_t D,
+                                   const void* q_in, int64_t q_len, int64_t q_in_bs, int64_t q_in_ls,
+                                   void* q_out, int64_t q_out_bs, int64_t q_out_ls,
+                                   const void* gamma_q, float eps_q,
+                                   const void* q_cos, const void* q_sin, int64_t q_tb, int64_t q_th,
+                                   int64_t q_tt,
+                                   const void* k_in, int64_t k_len, int64_t k_in_bs, int64_t k_in_ls,
+                                   void* k_out, int64_t k_out_bs, int64_t k_out_ls,
+                                   const void* gamma_k, float eps_k,
+                                   const void* k_cos, const void* k_sin, int64_t k_tb, int64_t k_th,
+                                   int64_t k_tt,
+                                   int tab_dtype, void* stream) {
+  clear_error();
+  LTX_REQUIRE(dtype == LTX_F32 || dtype == LTX_BF16, "ltx_qk_rmsnorm_rope: dtype must be F32 or BF16");
+  LTX_REQUIRE(tab_dtype == LTX_F32 || tab_dtype == LTX_BF16,
+              "ltx_qk_rmsnorm_rope: tab_dtype must be F32 or BF16");
+  LTX_REQUIRE(B >= 1 && B <= 65535 && H >= 1 && D >= 16 && D % 16 == 0,
+              "ltx_qk_rmsnorm_rope: need B in [1,65535], D a multiple of 16");
+  const int64_t threads = H * D / 16;
+  LTX_REQUIRE(threads <= 256 && threads % 64 == 0 || threads == 32 || threads == 16,
+              "ltx_qk_rmsnorm_rope: H*D/16 must be 16, 32 or a multiple of 64 up to 256 (H*D=%lld)",
+              (long long)(H * D));
+  LTX_REQUIRE(q_in && q_out && q_len >= 0, "ltx_qk_rmsnorm_rope: q pointers");
+  LTX_REQUIRE(!k_in || (k_out && k_len >= 0), "ltx_qk_rmsnorm_rope: k pointers");
+  LTX_REQUIRE((q_cos == nullptr) == (q_sin == nullptr) && (k_cos == nullptr) == (k_sin == nullptr),
+              "ltx_qk_rmsnorm_rope: cos and sin must both be given or both NULL");
+  const int64_t esz = dtype == LTX_BF16 ? 2 : 4;
+  auto aligned16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  LTX_REQUIRE(aligned16(q_in) && aligned16(q_out) && (!k_in || (aligned16(k_in) && aligned16(k_out))),
+              "ltx_qk_rmsnorm_rope: tensors must be 16-byte aligned");
+  LTX_REQUIRE((q_in_bs * esz) % 16 == 0 && (q_in_ls * esz) % 16 == 0 && (q_out_bs * esz) % 16 == 0 &&
+                  (q_out_ls * esz) % 16 == 0,
+              "ltx_qk_rmsnorm_rope: q strides must keep rows 16-byte aligned");
+  if (k_in)
+    LTX_REQUIRE((k_in_bs * esz) % 16 == 0 && (k_in_ls * esz) % 16 == 0 && (k_out_bs * esz) % 16 == 0 &&
+                    (k_out_ls * esz) % 16 == 0,
+                "ltx_qk_rmsnorm_rope: k strides must keep rows 16-byte aligned");
+  const int64_t tsz = tab_dtype == LTX_BF16 ? 2 : 4;
+  if (q_cos)
+    LTX_REQUIRE(aligned16(q_cos) && aligned16(q_sin) && (q_tb * tsz) % 16 == 0 && (q_th * tsz) % 16 == 0 &&
+                    (q_tt * tsz) % 16 == 0,
+                "ltx_qk_rmsnorm_rope: q tables must be 16-byte aligned");
+  if (k_cos)
+    LTX_REQUIRE(aligned16(k_cos) && aligned16(k_sin) && (k_tb * tsz) % 16 == 0 && (k_th * tsz) % 16 == 0 &&
+                    (k_tt * tsz) % 16 == 0,
+                "ltx_qk_rmsnorm_rope: k tables must be 16-byte aligned");
+  if (gamma_q) LTX_REQUIRE(aligned16(gamma_q), "ltx_qk_rmsnorm_rope: gamma_q alignment");
+  if (gamma_k) LTX_REQUIRE(aligned16(gamma_k), "ltx_qk_rmsnorm_rope: gamma_k alignment");
+
+  NormRopeSide qs{q_in, q_out, gamma_q, q_cos, q_sin, q_len, q_in_bs, q_in_ls, q_out_bs, q_out_ls,
+                  q_tb, q_th, q_tt, eps_q};
+  NormRopeSide ks{k_in, k_out, gamma_k, k_cos, k_sin, k_in ? k_len : 0, k_in_bs, k_in_ls, k_out_bs,
+                  k_out_ls, k_tb, k_th, k_tt, eps_k};
+  const int64_t rows = k_in ? (q_len > k_len ? q_len : k_len) : q_len;
+  if (rows == 0) return LTX_OK;
+  LTX_REQUIRE(rows <= 0x7FFFFFFF, "ltx_qk_rmsnorm_rope: too many rows");
+  const dim3 grid((unsigned)rows, (unsigned)B, k_in ? 2u : 1u);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == LTX_BF16) {
+    if (tab_dtype == LTX_BF16)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<uint16_t, uint16_t>), grid, dim3((unsigned)threads), 0,
+                         st, qs, ks, (int)H, (int)D);
+    else
+      hipLaunchKernelGGL((qk_norm_rope_kernel<uint16_t, float>), grid, dim3((unsigned)threads), 0, st,
+                         qs, ks, (int)H, (int)D);
+  } else {
+    if (tab_dtype == LTX_BF16)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<float, uint16_t>), grid, dim3((unsigned)threads), 0, st,
+                         qs, ks, (int)H, (int)D);
+    else
+      hipLaunchKernelGGL((qk_norm_rope_kernel<float, float>), grid, dim3((unsigned)threads), 0, st, qs,
+                         ks, (int)H, (int)D);
+  }
+  LTX_LAUNCH_CHECK("ltx_qk_rmsnorm_rope");
+  return LTX_OK;
+}

@@ -1,0 +1,256 @@
+"""GPU parity of each kernel against the CPU oracle (run on an MI355X)."""
+import math
+
+import pytest
+import torch
+
+from oracle import attention as OA
+from oracle import fp8 as OF
+from oracle import rope as OR
+from taomate_amd import kernels
+from taomate_amd.kernels import KVSegment
+from taomate_amd.rope import causal_precompute_freqs_cis, generate_freq_grid
+
+from .helpers import (BF16_MAX_ABS, BF16_MEAN_ABS, FP8_COSINE, assert_bf16_close, bf16_ulp_diff,
+                      cosine, diff_stats, gen, randn)
+
+pytestmark = pytest.mark.gpu
+
+ROPE_CASES = [
+    # (grid, dim, heads, start_frame, is_audio, max_pos)
+    ((2, 8, 12), 512, 8, 10, False, [20, 2048, 2048]),      # 8x12 latent grid, 8 x 64 heads
+    ((3, 16, 24), 4096, 32, 12, False, [20, 2048, 2048]),   # 16x24 grid, 32 x 128 heads
+    ((75,), 2048, 32, 600, True, [20]),                     # audio 1-D, 32 x 64
+    ((3,), 2048, 32, 12, False, [20]),                      # video-time 1-D (cross-modal)
+    ((4, 16, 24), 4096, 32, 0, False, [20, 2048, 2048]),    # frame 0 (causal fix clamp)
+]
+
+
+@pytest.mark.parametrize("case", ROPE_CASES, ids=lambda c: f"grid{c[0]}_dim{c[1]}")
+def test_rope_table_matches_oracle(dev, case):
+    grid, dim, heads, sf, audio, mp = case
+    gs = torch.tensor([list(grid)])
+    cos, sin = causal_precompute_freqs_cis(gs, dim, max_pos=mp, start_frame=sf, device=dev,
+                                           dtype=torch.float32, is_audio=audio,
+                                           num_attention_heads=heads)
+    rc, rs = OR.causal_precompute_freqs_cis(grid, dim, max_pos=mp, start_frame=sf, is_audio=audio,
+                                            num_attention_heads=heads)
+    assert cos.shape == rc.shape
+    # float32 tables: only the final cos/sin evaluation may differ (<= a few ulp)
+    assert (cos.cpu() - rc).abs().max().item() <= 2e-6
+    assert (sin.cpu() - rs).abs().max().item() <= 2e-6
+    # bf16 tables: rounding of those values; at most 1 bf16 ulp apart, nearly all equal
+    cb, sb = causal_precompute_freqs_cis(gs, dim, max_pos=mp, start_frame=sf, device=dev,
+                                         dtype=torch.bfloat16, is_audio=audio,
+                                         num_attention_heads=heads)
+    u = bf16_ulp_diff(cb, rc.to(torch.bfloat16))
+    assert u.max() <= 1 and (u == 0).mean() >= 0.999
+    u = bf16_ulp_diff(sb, rs.to(torch.bfloat16))
+    assert u.max() <= 1 and (u == 0).mean() >= 0.999
+
+
+def test_freq_grid_is_reference_expression(dev):
+    f = generate_freq_grid(10000.0, 3, 4096, dev).cpu()
+    assert torch.equal(f, OR.generate_freq_grid(10000.0, 3, 4096))
+
+
+NORM_CASES = [
+    # (B, L, H, D, dtype)
+    (1, 192, 8, 64, torch.bfloat16),
+    (2, 1152, 32, 128, torch.bfloat16),
+    (1, 75, 32, 64, torch.bfloat16),
+    (1, 192, 8, 64, torch.float32),
+    (2, 37, 16, 64, torch.float32),
+]
+
+
+@pytest.mark.parametrize("case", NORM_CASES, ids=lambda c: f"B{c[0]}L{c[1]}H{c[2]}D{c[3]}{str(c[4])[6:]}")
+def test_qk_rmsnorm_rope_matches_oracle(dev, case):
+    B, L, H, D, dt = case
+    g = gen(11)
+    HD = H * D
+    q = randn((B, L, HD), g, dt, 3.0)
+    k = randn((B, L, HD), g, dt, 0.5)
+    gq = (1 + 0.1 * randn((HD,), g)).to(dt)
+    gk = (1 + 0.1 * randn((HD,), g)).to(dt)
+    grid = (1, L, 1)
+    cos, sin = OR.causal_precompute_freqs_cis(grid, HD, start_frame=3, num_attention_heads=H,
+                                              batch=B, dtype=dt)
+    # oracle in the same dtype (the reference's composite op order) and in fp32
+    rq = OR.apply_split_rotary_emb(OA.rms_norm_full_row(q, gq, 1e-6), cos, sin)
+    rk = OR.apply_split_rotary_emb(OA.rms_norm_full_row(k, gk, 1e-6), cos, sin)
+    f = lambda t: t.float()
+    rq32 = OR.apply_split_rotary_emb(OA.rms_norm_full_row(f(q), f(gq), 1e-6), f(cos), f(sin))
+    qd, kd = q.to(dev), k.to(dev)
+    qo, ko = torch.empty_like(qd), torch.empty_like(kd)
+    kernels.qk_rmsnorm_rope(qd, qo, gq.to(dev), 1e-6, (cos.to(dev), sin.to(dev)), H, D,
+                            kd, ko, gk.to(dev), 1e-6, (cos.to(dev), sin.to(dev)))
+    torch.cuda.synchronize()
+    if dt == torch.bfloat16:
+        # same rounding sequence as torch's bf16 ops: bit-identical except where
+        # the float32 sum of squares (a different reduction order) flips a rounding
+        for out, ref in ((qo, rq), (ko, rk)):
+            out = out.cpu()
+            exact = (out == ref).float().mean().item()
+            d = (out.float() - ref.float()).abs().max().item()
+            assert exact >= 0.995 and d <= 2 ** -6 * ref.float().abs().max().item(), (exact, d)
+        assert_bf16_close(qo, rq32, "q vs fp32", max_abs=0.05, mean_abs=2e-3)
+    else:
+        assert diff_stats(qo, rq)[0] <= 1e-5
+        assert diff_stats(ko, rk)[0] <= 1e-5
+
+
+def test_norm_only_and_rope_only(dev):
+    g = gen(5)
+    B, L, H, D = 1, 64, 4, 64
+    x = randn((B, L, H * D), g, torch.bfloat16)
+    cos, sin = OR.causal_precompute_freqs_cis((1, L, 1), H * D, num_attention_heads=H, dtype=torch.bfloat16)
+    xd = x.to(dev)
+    y = torch.empty_like(xd)
+    kernels.qk_rmsnorm_rope(xd, y, None, 1e-6, None, H, D)
+    ref = OA.rms_norm_full_row(x, None, 1e-6)
+    assert (y.cpu() == ref).float().mean().item() >= 0.995
+    kernels.qk_rmsnorm_rope(xd, y, None, None, (cos.to(dev), sin.to(dev)), H, D)
+    ref = OR.apply_split_rotary_emb(x, cos, sin)
+    assert torch.equal(y.cpu(), ref)  # RoPE alone: the same three roundings, bit-exact
+
+
+def test_kv_append_copy_bit_exact(dev):
+    g = gen(3)
+    B, L, H, D = 2, 100, 32, 128
+    src = randn((B, L, H, D), g, torch.bfloat16).to(dev)
+    arena = torch.zeros(B, 300, H, D, dtype=torch.bfloat16, device=dev)
+    kernels.kv_append(src, arena[:, 57:57 + L])
+    torch.cuda.synchronize()
+    assert torch.equal(arena[:, 57:57 + L], src)
+    assert torch.count_nonzero(arena[:, :57]) == 0 and torch.count_nonzero(arena[:, 157:]) == 0
+
+
+@pytest.mark.parametrize("shape,frame", [((2, 1152, 32, 128), 384), ((1, 96, 8, 64), 96),
+                                          ((1, 50, 32, 64), 25)])
+def test_kv_append_fp8_bit_exact(dev, shape, frame):
+    g = gen(4)
+    B, L, H, D = shape
+    src = randn(shape, g, torch.bfloat16, 2.0)
+    src[0, :frame, 0] = 0  # an all-zero (b, h, frame): scale 1
+    codes_ref, sc_ref = OF.quantize_kv(src.float(), frame)
+    dst = torch.zeros(B, L, H, D, dtype=torch.uint8, device=dev)
+    sc = torch.zeros(B, H, L // frame, dtype=torch.float32, device=dev)
+    kernels.kv_append(src.to(dev), dst, sc, frame)
+    torch.cuda.synchronize()
+    assert torch.equal(sc.cpu(), sc_ref)
+    assert torch.equal(dst.cpu(), codes_ref)
+
+
+def test_kv_gather_bit_exact(dev):
+    g = gen(6)
+    B, L, H, D = 2, 500, 8, 64
+    src = randn((B, L, H, D), g, torch.bfloat16).to(dev)
+    spans = [(0, 96), (300, 0), (200, 150), (480, 20)]
+    dst = torch.empty(B, 266, H, D, dtype=torch.bfloat16, device=dev)
+    kernels.kv_gather(src, dst, spans)
+    ref = torch.cat([src[:, s:s + n] for s, n in spans], dim=1)
+    assert torch.equal(dst, ref)
+    u8 = torch.randint(0, 256, (B, L, H, D), dtype=torch.uint8, generator=g).to(dev)
+    d8 = torch.empty(B, 266, H, D, dtype=torch.uint8, device=dev)
+    kernels.kv_gather(u8, d8, spans)
+    assert torch.equal(d8, torch.cat([u8[:, s:s + n] for s, n in spans], dim=1))
+
+
+def _ref_attn(q, k, v, mask=None):
+    return OA.standard_attention_forward(q.float().cpu(), k.float().cpu(), v.float().cpu(),
+                                         None if mask is None else mask.cpu().view(mask.shape[0], 1, 1, -1))
+
+
+ATTN_CASES = [
+    # (B, Lq, H, D, segment lengths)
+    (1, 192, 8, 64, [96, 96, 384, 192]),          # 8x12 grid: anchor|memory|window|current
+    (2, 1152, 32, 128, [384, 768, 2304, 1152]),   # 16x24 grid full shape
+    (1, 75, 32, 64, [600, 75]),                   # audio self
+    (1, 1152, 32, 64, [75]),                      # A2V
+    (1, 75, 32, 64, [1152]),                      # V2A
+    (2, 130, 4, 128, [1, 63, 65, 7]),             # ragged tails, tiny segments
+    (1, 1, 2, 128, [5]),                          # single query / few keys
+]
+
+
+@pytest.mark.parametrize("case", ATTN_CASES, ids=lambda c: f"B{c[0]}q{c[1]}H{c[2]}D{c[3]}k{sum(c[4])}")
+def test_flash_attn_bf16_vs_fp32(dev, case):
+    B, Lq, H, D, lens = case
+    g = gen(7)
+    q = randn((B, Lq, H, D), g, torch.bfloat16)
+    ks = [randn((B, n, H, D), g, torch.bfloat16) for n in lens]
+    vs = [randn((B, n, H, D), g, torch.bfloat16) for n in lens]
+    # segments live in one arena with shared strides, at scattered slots
+    cap = sum(lens) + 64 * len(lens)
+    ka = torch.zeros(B, cap, H, D, dtype=torch.bfloat16, device=dev)
+    va = torch.zeros_like(ka)
+    segs, pos = [], 0
+    for kk, vv in zip(ks, vs):
+        n = kk.shape[1]
+        ka[:, pos:pos + n] = kk.to(dev)
+        va[:, pos:pos + n] = vv.to(dev)
+        segs.append(KVSegment(ka[:, pos:pos + n], va[:, pos:pos + n]))
+        pos += n + 37  # gaps between spans
+    out = torch.empty(B, Lq, H, D, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(B, H, Lq, dtype=torch.float32, device=dev)
+    kernels.flash_attn(q.to(dev), segs, out, lse=lse)
+    torch.cuda.synchronize()
+    K, V = torch.cat(ks, 1), torch.cat(vs, 1)
+    ref = _ref_attn(q, K, V)
+    assert_bf16_close(out, ref, f"attn {case}")
+    s = torch.einsum("bqhd,bkhd->bhqk", q.float(), K.float()) / math.sqrt(D)
+    assert (lse.cpu() - torch.logsumexp(s, -1)).abs().max().item() < 1e-2
+
+
+def test_flash_attn_key_mask(dev):
+    """Text cross-attention: 1152 queries, 1024 keys, 20% masked with the
+    reference's (m-1)*finfo.max additive mask."""
+    g = gen(8)
+    B, Lq, Lk, H, D = 1, 1152, 1024, 32, 128
+    q = randn((B, Lq, H, D), g, torch.bfloat16)
+    k = randn((B, Lk, H, D), g, torch.bfloat16)
+    v = randn((B, Lk, H, D), g, torch.bfloat16)
+    keep = torch.ones(B, Lk, dtype=torch.int64)
+    keep[:, -int(0.2 * Lk):] = 0
+    add = OA.prepare_attention_mask(keep, torch.bfloat16)          # [B,1,1,Lk] bf16
+    ref = OA.standard_attention_forward(q.float(), k.float(), v.float(), add.float())
+    out = torch.empty(B, Lq, H, D, dtype=torch.bfloat16, device=dev)
+    kernels.flash_attn(q.to(dev), [KVSegment(k.to(dev), v.to(dev))], out,
+                       key_mask=add.view(B, Lk).float().to(dev))
+    torch.cuda.synchronize()
+    assert_bf16_close(out, ref, "masked attn")
+    # masking equals dropping the masked keys
+    kept = int(keep.sum())
+    ref2 = OA.standard_attention_forward(q.float(), k[:, :kept].float(), v[:, :kept].float())
+    assert_bf16_close(out, ref2, "masked == removed")
+
+
+@pytest.mark.parametrize("case", [(2, 1152, 32, 128, 384, [384, 768, 2304, 1152]),
+                                  (1, 192, 8, 64, 64, [128, 64, 384, 192])],
+                         ids=["16x24grid", "8x12grid"])
+def test_flash_attn_fp8_kv(dev, case):
+    B, Lq, H, D, frame, lens = case
+    g = gen(9)
+    q = randn((B, Lq, H, D), g, torch.bfloat16)
+    K = randn((B, sum(lens), H, D), g, torch.bfloat16)
+    V = randn((B, sum(lens), H, D), g, torch.bfloat16)
+    kc, ksc = OF.quantize_kv(K.float(), frame)
+    vc, vsc = OF.quantize_kv(V.float(), frame)
+    kc, vc, ksc, vsc = kc.to(dev), vc.to(dev), ksc.to(dev), vsc.to(dev)
+    segs, pos = [], 0
+    for n in lens:
+        f0, nf = pos // frame, n // frame
+        segs.append(KVSegment(kc[:, pos:pos + n], vc[:, pos:pos + n], ksc[:, :, f0:f0 + nf],
+                              vsc[:, :, f0:f0 + nf]))
+        pos += n
+    out = torch.empty(B, Lq, H, D, dtype=torch.bfloat16, device=dev)
+    kernels.flash_attn(q.to(dev), segs, out, frame_tokens=frame)
+    torch.cuda.synchronize()
+    ref = _ref_attn(q, K, V)
+    c = cosine(out, ref)
+    assert c >= FP8_COSINE, c
+    # against the dequantised cache the only error left is bf16 rounding
+    Kd = OF.dequantize_kv(kc.cpu(), ksc.cpu(), frame)
+    Vd = OF.dequantize_kv(vc.cpu(), vsc.cpu(), frame)
+    assert_bf16_close(out, _ref_attn(q, Kd, Vd), "fp8 vs dequantised")

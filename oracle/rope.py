@@ -76,6 +76,24 @@ def _fractional_positions(grid: Tuple[int, ...], start_frame: int, is_audio: boo
     return (t_sec / max_pos[0]).unsqueeze(-1)
 
 
+def rope_angles(grid: Tuple[int, ...], dim: int, theta: float = 10000.0,
+                max_pos: Optional[List[int]] = None, start_frame: int = 0,
+                is_audio: bool = False, rope_extrapolation: str = "off",
+                rope_train_max_seconds: float = 8.0) -> Tuple[torch.Tensor, int]:
+    """causal_rope.py:249-321: float32 angles [T, n*ndim] interleaved
+    [f0_t, f0_h, f0_w, f1_t, ...] (before the SPLIT pad), and the pad size."""
+    if max_pos is None:
+        max_pos = [20, 2048, 2048]
+    ndim = len(grid)
+    th = ntk_theta(theta, dim, grid[0], start_frame, is_audio, rope_extrapolation,
+                   rope_train_max_seconds)
+    ind = generate_freq_grid(th, ndim, dim)                        # [n]
+    frac = _fractional_positions(grid, start_frame, is_audio, max_pos)  # [T, ndim]
+    freqs = ind * (frac.unsqueeze(-1) * 2 - 1)                     # [T, ndim, n]
+    freqs = freqs.transpose(-1, -2).flatten(1)                      # [T, n*ndim]
+    return freqs, dim // 2 - freqs.shape[-1]
+
+
 def causal_precompute_freqs_cis(grid: Tuple[int, ...], dim: int, theta: float = 10000.0,
                                 max_pos: Optional[List[int]] = None, start_frame: int = 0,
                                 dtype: torch.dtype = torch.float32, is_audio: bool = False,
@@ -89,17 +107,9 @@ def causal_precompute_freqs_cis(grid: Tuple[int, ...], dim: int, theta: float = 
     so a B=2 input pairs with a B=2 table (the reference's split helper reshapes
     x with the *table's* batch, :111-115).
     """
-    if max_pos is None:
-        max_pos = [20, 2048, 2048]
-    ndim = len(grid)
-    th = ntk_theta(theta, dim, grid[0], start_frame, is_audio, rope_extrapolation,
-                   rope_train_max_seconds)
-    ind = generate_freq_grid(th, ndim, dim)                        # [n]
-    frac = _fractional_positions(grid, start_frame, is_audio, max_pos)  # [T, ndim]
-    freqs = ind * (frac.unsqueeze(-1) * 2 - 1)                     # [T, ndim, n]
-    freqs = freqs.transpose(-1, -2).flatten(1)                      # [T, n*ndim]
+    freqs, pad = rope_angles(grid, dim, theta, max_pos, start_frame, is_audio,
+                             rope_extrapolation, rope_train_max_seconds)
     cos, sin = freqs.cos(), freqs.sin()
-    pad = dim // 2 - freqs.shape[-1]
     if pad > 0:
         cos = torch.cat([torch.ones_like(cos[:, :pad]), cos], dim=-1)
         sin = torch.cat([torch.zeros_like(sin[:, :pad]), sin], dim=-1)

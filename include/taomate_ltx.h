@@ -100,22 +100,27 @@ int ltx_qk_rmsnorm_rope(int dtype, int64_t B, int64_t H, int64_t D,
                         int tab_dtype, void* stream);
 
 /*
- * KV append into a preallocated arena (copy or fp8 quantise).
+ * KV append into a preallocated arena (copy, transpose or fp8 quantise).
  * Replaces _cat_cache / torch.cat (ltx_causal/transformer/kv_cache.py:394-398,
  * block cache update :2642-2656): the new tokens are written once into their
  * arena slots instead of reallocating the whole cache.
- *   src: [B, L, H, D] `src_dtype` (LTX_BF16 or LTX_F32), strides (bs, ls, hs).
- *   dst: [B, L, H, D] `dst_dtype` strides (bs, ls, hs). dst_dtype LTX_BF16 copies;
- *   LTX_F8E4M3 quantises with one scale per (b, h, frame) of `frame_tokens`
- *   tokens: scale = absmax / 448 (1 if absmax == 0), q = rne_sat(x / scale).
+ *   src: [B, L, H, D] `src_dtype` (LTX_BF16 or LTX_F32), strides (bs, ls, hs),
+ *   D contiguous.
+ *   dst: element (b, l, h, d) at dst + b*d_bs + l*d_ls + h*d_hs + d*d_ds.
+ *     d_ds == 1: token-major; dst_dtype LTX_BF16 copies, LTX_F8E4M3 quantises
+ *       with one scale per (b, h, frame) of `frame_tokens` tokens:
+ *       scale = absmax / 448 (1 if absmax == 0), q = rne_sat(x / scale).
+ *     d_ls == 1: key-major (the arena's V layout, [B, H, D, slots]); LTX_BF16
+ *       only: the tokens are transposed on the way in.
  *   scales: float32 [B, H, n_frames] with strides (sbs, shs), frame index f
  *   at scales[b*sbs + h*shs + f]; only used for LTX_F8E4M3. L must be a
  *   multiple of frame_tokens for LTX_F8E4M3.
  */
 int ltx_kv_append(int src_dtype, int dst_dtype, int64_t B, int64_t L, int64_t H,
                   int64_t D, const void* src, int64_t s_bs, int64_t s_ls, int64_t s_hs,
-                  void* dst, int64_t d_bs, int64_t d_ls, int64_t d_hs, float* scales,
-                  int64_t sc_bs, int64_t sc_hs, int64_t frame_tokens, void* stream);
+                  void* dst, int64_t d_bs, int64_t d_ls, int64_t d_hs, int64_t d_ds,
+                  float* scales, int64_t sc_bs, int64_t sc_hs, int64_t frame_tokens,
+                  void* stream);
 
 /*
  * Span gather (cache compaction).
@@ -139,27 +144,47 @@ int ltx_kv_gather(int64_t elem_bytes, int64_t B, int64_t H, int64_t D, const voi
  * kv_cache.py:1531): out = softmax(q k^T * scale + mask) v over the keys of all
  * segments in order; no causal mask (causality is what the segments contain).
  *   q, out: [B, Lq, H, D] bf16, strides (bs, ls, hs).  D in {64, 128}.
- *   Segment i: k_ptrs[i], v_ptrs[i] point at its first token (b=0, h=0);
- *   seg_lens[i] tokens; all segments share kv strides (bs, ls, hs).
- *   kv_dtype LTX_BF16, or LTX_F8E4M3 with per-(b, h, frame) float32 scales:
- *   k_scales[i], v_scales[i] for segment i, index b*sc_bs + h*sc_hs + (t/frame)
- *   where t counts tokens from the segment start.
+ *   Segment i: k_ptrs[i], v_ptrs[i] point at its first token (b=0, h=0, d=0);
+ *   seg_lens[i] tokens.  K element (b, t, h, d) at k + b*k_bs + t*k_ls + h*k_hs
+ *   + d; V element at v + b*v_bs + t*v_ls + h*v_hs + d*v_ds, either token-major
+ *   (v_ds == 1) or key-major (v_ls == 1, bf16 only).  All segments share the
+ *   strides.  Key-major V is read in 8-token (16-byte) chunks: a segment's
+ *   start must be 16-byte aligned and its values may be read up to the next
+ *   multiple of 8 tokens past its end; those extra values must be finite (they
+ *   get weight 0).  The KV arena guarantees both.
+ *   kv_dtype LTX_BF16, or LTX_F8E4M3 (token-major) with per-(b, h, frame)
+ *   float32 scales: k_scales[i], v_scales[i] for segment i, index b*sc_bs +
+ *   h*sc_hs + (t/frame) where t counts tokens from the segment start.
  *   key_mask: NULL or float32 additive mask [B, Lk_total] with batch stride
  *   mask_bs (the reference's `(m - 1) * finfo.max` padding mask,
- *   ltx_causal/transformer/causal_model.py:551-562).
+ *   ltx_causal/transformer/causal_model.py:551-562); token-major V only.
  *   lse: NULL or float32 [B, H, Lq] natural-log sum-exp of the scaled logits.
  *   scale <= 0 selects 1/sqrt(D) (SDPA's default).
+ *   workspace: NULL, or workspace_bytes >= ltx_flash_attn_workspace_size() of
+ *   device memory, 256-byte aligned.  With it the q-tiles that do not fill a
+ *   whole round of the device's resident workgroups are split along the keys
+ *   and recombined by a second kernel on `stream`, so the grid ends together;
+ *   without it they run whole.  Calls that overlap in time must use different
+ *   workspaces.
  *   Host arrays (k_ptrs, v_ptrs, seg_lens, scales) are read during the call only.
  */
 int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t H, int64_t D,
                        int64_t q_bs, int64_t q_ls, int64_t q_hs, int64_t n_segments,
                        const void* const* k_ptrs, const void* const* v_ptrs,
-                       const int64_t* seg_lens, int64_t kv_bs, int64_t kv_ls,
-                       int64_t kv_hs, int kv_dtype, const float* const* k_scales,
-                       const float* const* v_scales, int64_t sc_bs, int64_t sc_hs,
-                       int64_t frame_tokens, const float* key_mask, int64_t mask_bs,
-                       void* out, int64_t o_bs, int64_t o_ls, int64_t o_hs, float* lse,
-                       float scale, void* stream);
+                       const int64_t* seg_lens, int64_t k_bs, int64_t k_ls, int64_t k_hs,
+                       int64_t v_bs, int64_t v_ls, int64_t v_hs, int64_t v_ds, int kv_dtype,
+                       const float* const* k_scales, const float* const* v_scales,
+                       int64_t sc_bs, int64_t sc_hs, int64_t frame_tokens,
+                       const float* key_mask, int64_t mask_bs, void* out, int64_t o_bs,
+                       int64_t o_ls, int64_t o_hs, float* lse, float scale, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+
+/*
+ * Workspace bytes ltx_flash_attn_fwd can use for a [B, Lq, H, D] query on the
+ * current device (0: no split is ever planned for this shape).
+ * No counterpart in the reference (its SDPA call has no workspace).
+ */
+int ltx_flash_attn_workspace_size(int64_t B, int64_t Lq, int64_t H, int64_t D, int64_t* bytes);
 
 #ifdef __cplusplus
 }

@@ -36,12 +36,13 @@ SIGNATURES = {
                             _i64, _i64,
                             _int, _ptr],
     "ltx_kv_append": [_int, _int, _i64, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64,
-                      _i64, _ptr, _i64, _i64, _i64, _ptr],
+                      _i64, _i64, _ptr, _i64, _i64, _i64, _ptr],
     "ltx_kv_gather": [_i64, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _i64,
                       _ptr, _ptr, _ptr],
     "ltx_flash_attn_fwd": [_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr,
-                           _i64, _i64, _i64, _int, _ptr, _ptr, _i64, _i64, _i64, _ptr, _i64, _ptr,
-                           _i64, _i64, _i64, _ptr, _f32, _ptr],
+                           _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _ptr, _ptr, _i64, _i64,
+                           _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _ptr, _f32, _ptr, _i64, _ptr],
+    "ltx_flash_attn_workspace_size": [_i64, _i64, _i64, _i64, _ptr],
 }
 
 

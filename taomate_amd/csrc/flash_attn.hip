@@ -45,7 +45,8 @@ struct FlashParams {
   const float* mask;
   int64_t q_bs, q_ls, q_hs;
   int64_t o_bs, o_ls, o_hs;
-  int64_t kv_bs, kv_ls, kv_hs;
+  int64_t kv_bs, kv_ls, kv_hs;      // K (and token-major V) strides
+  int64_t v_bs, v_hs, v_ds;          // key-major V: element (b, t, h, d) at b*v_bs + h*v_hs + d*v_ds + t
   int64_t sc_bs, sc_hs;
   int64_t mask_bs;
   int64_t Lk;
@@ -56,9 +57,26 @@ struct FlashParams {
   const float* v_sc[LTX_MAX_SEGMENTS];
   int tile_start[LTX_MAX_SEGMENTS + 1];  // first key tile of each segment (cumulative)
   int B, H, Lq, n_seg, n_qtiles, frame;
+  // Balanced tail: the first n_full q-tiles run whole; each of the remaining
+  // q-tiles is cut into `split` key ranges run by separate workgroups, whose
+  // partial results meet in the workspace and are combined by a second kernel.
+  int n_full, split;
+  float* part_o;    // [tail tiles * split][kBM][D] unnormalised O
+  float* part_ml;   // [tail tiles * split][kBM][2] running max (log2) and sum
   float scale;       // softmax scale applied to q.k
   float scale_log2;  // scale * log2(e)
 };
+
+// Max / sum of a lane's value with lane l ^ 32's (the lane holding the other
+// 16 keys of the same query): one v_permlane32_swap, no LDS round trip.
+__device__ __forceinline__ float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 constexpr int kBM = 128;
 constexpr int kBN = 64;
@@ -147,7 +165,121 @@ struct TileIter {
   __device__ __forceinline__ int nvalid() const {
     return (int)(len - row0 < kBN ? len - row0 : kBN);
   }
+  // position on key tile j of the concatenated sequence
+  __device__ __forceinline__ void seek(const FlashParams& p, int j) {
+    int seg = 0;
+    for (int i = 1; i < p.n_seg; ++i) seg = (j >= p.tile_start[i]) ? i : seg;
+    enter(p, seg);
+    row0 = (int64_t)(j - p.tile_start[seg]) * kBN;
+    key0 += row0;
+  }
 };
+
+// Which q-tile and key-tile range block `bid` owns.  Blocks below n_full take
+// whole q-tiles; the rest take 1/split of a tail q-tile's key tiles.  Each
+// group is spread over the 8 XCDs on its own (dispatch is round-robin by
+// block id), and inside a group consecutive work shares an XCD's L2.
+struct WorkItem {
+  int qtile;   // linear (b*H + h) * n_qtiles + qt
+  int j0, j1;  // key tiles [j0, j1)
+  int piece;   // -1: whole q-tile; else index into the partial buffers
+  int tail;    // tail q-tile index (piece >= 0)
+};
+__device__ __forceinline__ WorkItem work_item(const FlashParams& p, int bid, int ntiles) {
+  WorkItem w;
+  if (bid < p.n_full) {
+    w.qtile = xcd_remap(bid, p.n_full);
+    w.j0 = 0;
+    w.j1 = ntiles;
+    w.piece = -1;
+    w.tail = -1;
+  } else {
+    const int ntail = gridDim.x - p.n_full;
+    const int t = xcd_remap(bid - p.n_full, ntail);
+    w.tail = t / p.split;
+    const int part = t % p.split;
+    w.qtile = p.n_full + w.tail;
+    w.j0 = (int)((int64_t)ntiles * part / p.split);
+    w.j1 = (int)((int64_t)ntiles * (part + 1) / p.split);
+    w.piece = t;
+  }
+  return w;
+}
+
+// Epilogue shared by the kernels: normalise and store a whole q-tile, or
+// store a key range's partial result (unnormalised O, running max and sum).  oacc holds O^T fragments (lane: query li,
+// d = db*32 + 8*(r/4) + 4*hg + r%4); m_run / l_tot are per query.
+template <int D>
+__device__ __forceinline__ void finish_tile(const FlashParams& p, const WorkItem& w, int b, int h,
+                                            int qt, const f32x16_t (&oacc)[D / 32], float m_run,
+                                            float l_tot) {
+  constexpr int DB = D / 32;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int li = lane & 31, hg = lane >> 5;
+  const int row = wave * 32 + li;  // row inside the q-tile
+  const int qi = qt * kBM + row;
+  if (w.piece < 0) {
+    if (qi < p.Lq) {
+      const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+      uint16_t* op = p.o + b * p.o_bs + (int64_t)qi * p.o_ls + h * p.o_hs;
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          uint2 v;
+          v.x = pack_bf16x2(oacc[d][4 * g4] * inv, oacc[d][4 * g4 + 1] * inv);
+          v.y = pack_bf16x2(oacc[d][4 * g4 + 2] * inv, oacc[d][4 * g4 + 3] * inv);
+          *reinterpret_cast<uint2*>(op + d * 32 + 8 * g4 + 4 * hg) = v;
+        }
+      }
+      if (p.lse != nullptr && hg == 0) p.lse[((int64_t)b * p.H + h) * p.Lq + qi] = (m_run + __log2f(l_tot)) / kLog2e;
+    }
+    return;
+  }
+  // ---- partial result of one key range: combined by flash_combine_kernel ----
+  float* po = p.part_o + ((int64_t)w.piece * kBM + row) * D;
+#pragma unroll
+  for (int d = 0; d < DB; ++d)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4)
+      *reinterpret_cast<float4*>(po + d * 32 + 8 * g4 + 4 * hg) =
+          make_float4(oacc[d][4 * g4], oacc[d][4 * g4 + 1], oacc[d][4 * g4 + 2], oacc[d][4 * g4 + 3]);
+  if (hg == 0) *reinterpret_cast<float2*>(p.part_ml + ((int64_t)w.piece * kBM + row) * 2) = make_float2(m_run, l_tot);
+}
+
+// Combines the `split` partial results of every tail q-tile: one workgroup per
+// tail q-tile, launched after the attention kernel on the same stream.
+template <int D>
+__global__ void __launch_bounds__(256) flash_combine_kernel(const FlashParams p) {
+  const int tail = blockIdx.x;
+  const int qtile = p.n_full + tail;
+  const int qt = qtile % p.n_qtiles;
+  const int bh = qtile / p.n_qtiles;
+  const int b = bh / p.H, h = bh % p.H;
+  const int first = tail * p.split;
+  for (int idx = threadIdx.x; idx < kBM * (D / 4); idx += blockDim.x) {
+    const int r = idx / (D / 4), c4 = idx % (D / 4);
+    const int q = qt * kBM + r;
+    if (q >= p.Lq) continue;
+    float mmax = -INFINITY;
+    for (int i = 0; i < p.split; ++i) mmax = fmaxf(mmax, p.part_ml[((int64_t)(first + i) * kBM + r) * 2]);
+    float lsum = 0.0f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < p.split; ++i) {
+      const float2 ml = *reinterpret_cast<const float2*>(p.part_ml + ((int64_t)(first + i) * kBM + r) * 2);
+      const float wgt = __builtin_amdgcn_exp2f(ml.x - mmax);
+      lsum += wgt * ml.y;
+      const float4 o = *reinterpret_cast<const float4*>(p.part_o + ((int64_t)(first + i) * kBM + r) * D + c4 * 4);
+      acc.x += wgt * o.x; acc.y += wgt * o.y; acc.z += wgt * o.z; acc.w += wgt * o.w;
+    }
+    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+    uint2 v;
+    v.x = pack_bf16x2(acc.x * inv, acc.y * inv);
+    v.y = pack_bf16x2(acc.z * inv, acc.w * inv);
+    *reinterpret_cast<uint2*>(p.o + b * p.o_bs + (int64_t)q * p.o_ls + h * p.o_hs + c4 * 4) = v;
+    if (p.lse != nullptr && c4 == 0) p.lse[((int64_t)b * p.H + h) * p.Lq + q] = (mmax + __log2f(lsum)) / kLog2e;
+  }
+}
 
 template <int D, bool FP8, bool MASK>
 __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(const FlashParams p) {
@@ -168,14 +300,14 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(const FlashParams p) 
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (KBUF + VBUF)];
   __shared__ float mask_s[MASK ? 2 : 1][MASK ? BN : 1];
 
-  const int linear = xcd_remap(blockIdx.x, gridDim.x);
-  const int qt = linear % p.n_qtiles;
-  const int bh = linear / p.n_qtiles;
+  const WorkItem wi = work_item(p, blockIdx.x, p.tile_start[p.n_seg]);
+  const int qt = wi.qtile % p.n_qtiles;
+  const int bh = wi.qtile / p.n_qtiles;
   const int b = bh / p.H, h = bh % p.H;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int li = lane & 31, hg = lane >> 5;
   const int qi = qt * BM + wave * 32 + li;
-  const int ntiles = p.tile_start[p.n_seg];
+  const int ntiles = wi.j1 - wi.j0;
 
   // ---- Q^T fragments, resident for the whole key loop ----
   bf16x8_t qf[QS];
@@ -209,7 +341,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(const FlashParams p) 
   raw_t vreg[4];
   float mreg = 0.0f;
   TileIter ld;
-  ld.enter(p, 0);
+  ld.seek(p, wi.j0);
   auto load_tile = [&]() {
     const int64_t base = (kv_off + ld.row0 * p.kv_ls) * ESZ;
     const int nbytes = ld.nvalid() * row_bytes;
@@ -278,7 +410,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(const FlashParams p) 
     __syncthreads();
   }
   TileIter cp;
-  cp.enter(p, 0);
+  cp.seek(p, wi.j0);
 
   for (int j = 0; j < ntiles; ++j) {
     const int buf = j & 1;
@@ -345,7 +477,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(const FlashParams p) 
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[kb][r]);
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    mt = pair_max(mt);
     // logits are x = s * c (c > 0), so max(x) = max(s) * c
     const float c = MASK ? 1.0f : c_log2;
     const float m_tile = mt * c;
@@ -359,7 +491,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(const FlashParams p) 
       for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
     }
     // all keys masked so far: keep the exponent finite
-    const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
+    const float neg_m = (m_run == -INFINITY) ? 0.0f : -m_run;
 
     float psum = 0.0f;
     bf16x8_t pf[4];
@@ -369,8 +501,8 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(const FlashParams p) 
       uint32_t w[4];
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][8 * t + e], c, -m_use));
-        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][8 * t + e + 1], c, -m_use));
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][8 * t + e], c, neg_m));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][8 * t + e + 1], c, neg_m));
         psum += p0 + p1;
         w[e >> 1] = FP8 ? pack_bf16x2(p0 * v_scale, p1 * v_scale) : pack_bf16x2(p0, p1);
       }
@@ -400,50 +532,394 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(const FlashParams p) 
     __syncthreads();
   }
 
-  // ---- epilogue: combine the two lane halves' sums, normalise, store ----
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  if (qi < p.Lq) {
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    uint16_t* op = p.o + b * p.o_bs + (int64_t)qi * p.o_ls + h * p.o_hs;
+  // ---- epilogue: combine the two lane halves' sums, then store or publish ----
+  finish_tile<D>(p, wi, b, h, qt, oacc, m_run, pair_sum(l_run));
+}
+
+// ---------------------------------------------------------------------------
+// Direct-to-LDS variant (bf16; K token-major, V key-major in HBM).
+//
+// gfx950 buffer loads can write 16 bytes per lane straight into LDS (lane L of
+// an instruction lands at base + 16*L).  Each instruction therefore covers 64
+// consecutive 16-byte LDS chunks of a padded tile: a K row is 16 data chunks
+// plus 1 pad chunk (the same 272-byte rows as the register-staged kernel), a
+// V^T row (one head-dim channel, 64 keys) 8 data chunks plus 1 pad.  Lanes
+// that fall on a pad chunk re-read a valid chunk.  The K-row order swap and
+// the V transpose both happen in the address each lane reads from, so no
+// registers and no VALU work go into staging.  V must be stored key-major
+// (the KV arena's V layout); a segment's last 8-token chunk is read whole,
+// its keys past the segment end are masked out of the softmax.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+template <int D, bool PIPE>
+__global__ void __launch_bounds__(256, 2) flash_fwd_direct_kernel(const FlashParams p) {
+  constexpr int BM = kBM, BN = kBN;
+  constexpr int NKC = D / 8;                 // data chunks per K row
+  constexpr int KS = D + 8;                  // padded K row (elements)
+  constexpr int VS = BN + 8;                 // padded V^T row (elements)
+  constexpr int KBUF = BN * KS;
+  constexpr int VBUF = D * VS;
+  constexpr int KINS = BN * (NKC + 1) / 64;  // load instructions per K tile
+  constexpr int VINS = D * 9 / 64;           // load instructions per V^T tile
+  constexpr int KSLOT = (KINS + 3) / 4;      // per wave
+  constexpr int VSLOT = (VINS + 3) / 4;
+  constexpr int DB = D / 32;
+  constexpr int QS = D / 16;
+  static_assert(BN * (NKC + 1) % 64 == 0 && D * 9 % 64 == 0, "tile does not split into whole instructions");
+
+  __shared__ __attribute__((aligned(16))) uint16_t kbuf[2][KBUF];
+  __shared__ __attribute__((aligned(16))) uint16_t vbuf[2][VBUF];
+
+  const WorkItem wi = work_item(p, blockIdx.x, p.tile_start[p.n_seg]);
+  const int qt = wi.qtile % p.n_qtiles;
+  const int bh = wi.qtile / p.n_qtiles;
+  const int b = bh / p.H, h = bh % p.H;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int li = lane & 31, hg = lane >> 5;
+  const int qi = qt * BM + wave * 32 + li;
+  const int ntiles = wi.j1 - wi.j0;
+
+  bf16x8_t qf[QS];
+  {
+    const bool ok = qi < p.Lq;
+    const uint16_t* qp = p.q + b * p.q_bs + (int64_t)(ok ? qi : 0) * p.q_ls + h * p.q_hs + hg * 8;
+#pragma unroll
+    for (int s = 0; s < QS; ++s) {
+      uint4 v = ok ? *reinterpret_cast<const uint4*>(qp + s * 16) : make_uint4(0, 0, 0, 0);
+      qf[s] = __builtin_bit_cast(bf16x8_t, v);
+    }
+  }
+
+  // Per-lane source offsets (bytes from the tile's first key) of every load
+  // instruction this wave issues; loop invariant.  krow/vchk keep the row and
+  // chunk so the last, partial tile of a segment can clamp them.
+  const int row_bytes = (int)(p.kv_ls * 2);
+  int koff[KSLOT], voff[VSLOT];
+  // (row, chunk) of this lane's chunk in instruction slot i, pad chunks mapped
+  // onto a data chunk; recomputed only for a segment's partial last tile
+  auto kpos = [&](int i, int& r, int& c) {
+    const int pch = (wave + 4 * i) * 64 + lane;
+    r = sig(pch / (NKC + 1));
+    c = pch % (NKC + 1);
+    c = c < NKC ? c : 0;
+  };
+  auto vpos = [&](int i, int& d, int& c) {
+    const int pch = (wave + 4 * i) * 64 + lane;
+    d = pch / 9;
+    d = d < D ? d : 0;
+    c = pch % 9;
+    c = c < 8 ? c : 0;
+  };
+#pragma unroll
+  for (int i = 0; i < KSLOT; ++i) {
+    int r, c;
+    kpos(i, r, c);
+    koff[i] = r * row_bytes + c * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < VSLOT; ++i) {
+    int d, c;
+    vpos(i, d, c);
+    voff[i] = (int)(d * p.v_ds * 2) + c * 16;
+  }
+
+  const int64_t k_off = b * p.kv_bs + h * p.kv_hs;
+  const int64_t v_off = b * p.v_bs + h * p.v_hs;
+  TileIter kit, vit;
+  kit.seek(p, wi.j0);
+  vit.seek(p, wi.j0);
+  auto issue_k = [&](int buf) {
+    const char* base = reinterpret_cast<const char*>(kit.k) + (k_off + kit.row0 * p.kv_ls) * 2;
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, 0x7FFFFFFF, 0x00020000);
+    const int nv = kit.nvalid();
+#pragma unroll
+    for (int i = 0; i < KSLOT; ++i) {
+      const int q = wave + 4 * i;
+      if (q < KINS) {
+        int off = koff[i];
+        if (nv < BN) {
+          int r, c;
+          kpos(i, r, c);
+          off = min(r, nv - 1) * row_bytes + c * 16;
+        }
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(&kbuf[buf][q * 512]), 16, off, 0, 0, 0);
+      }
+    }
+    kit.next(p);
+  };
+  auto issue_v = [&](int buf) {
+    const char* base = reinterpret_cast<const char*>(vit.v) + (v_off + vit.row0) * 2;
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, 0x7FFFFFFF, 0x00020000);
+    const int nv = vit.nvalid();
+#pragma unroll
+    for (int i = 0; i < VSLOT; ++i) {
+      const int q = wave + 4 * i;
+      if (q < VINS) {
+        int off = voff[i];
+        if (nv < BN) {
+          int d, c;
+          vpos(i, d, c);
+          off = (int)(d * p.v_ds * 2) + min(c, (nv + 7) / 8 - 1) * 16;
+        }
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(&vbuf[buf][q * 512]), 16, off, 0, 0, 0);
+      }
+    }
+    vit.next(p);
+  };
+  auto qk = [&](int buf, f32x16_t (&acc)[2]) {
+    acc[0] = f32x16_t{};
+    acc[1] = f32x16_t{};
+    const uint16_t* kfrag = &kbuf[buf][li * KS + hg * 8];
+    bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(kfrag);
+    bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(kfrag + 32 * KS);
+#pragma unroll
+    for (int s = 0; s < QS; ++s) {
+      bf16x8_t n0 = a0, n1 = a1;
+      if (s + 1 < QS) {
+        n0 = *reinterpret_cast<const bf16x8_t*>(kfrag + (s + 1) * 16);
+        n1 = *reinterpret_cast<const bf16x8_t*>(kfrag + 32 * KS + (s + 1) * 16);
+      }
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[s], acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[s], acc[1], 0, 0, 0);
+      a0 = n0;
+      a1 = n1;
+    }
+  };
+
+  f32x16_t oacc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) oacc[d] = f32x16_t{};
+  constexpr float kLazy = 8.0f;
+  const float c = p.scale_log2;
+  float m_run = -INFINITY;
+  float l_run = 0.0f;
+
+  // softmax of one tile's S^T accumulators into bf16 P fragments
+  auto softmax = [&](f32x16_t (&sacc)[2], int nvalid, bf16x8_t (&pf)[4]) {
+    if (nvalid < BN) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb * 32 + 16 * (r >> 3) + 8 * hg + (r & 7);
+          if (key >= nvalid) sacc[kb][r] = -INFINITY;
+        }
+    }
+    float mt = sacc[0][0];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[kb][r]);
+    const float m_tile = pair_max(mt) * c;
+    if (__builtin_amdgcn_ballot_w64(m_tile > m_run + kLazy)) {
+      const float m_new = fmaxf(m_run, m_tile);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
+    }
+    const float neg_m = -m_run;
+    float psum = 0.0f;
+#pragma unroll
+    for (int ks4 = 0; ks4 < 4; ++ks4) {
+      const int kb = ks4 >> 1, t = ks4 & 1;
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][8 * t + e], c, neg_m));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][8 * t + e + 1], c, neg_m));
+        psum += p0 + p1;
+        w[e >> 1] = pack_bf16x2(p0, p1);
+      }
+      pf[ks4] = __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
+    }
+    l_run += psum;
+  };
+  auto pv = [&](int buf, const bf16x8_t (&pf)[4]) {
+    const uint16_t* vfrag = &vbuf[buf][li * VS + hg * 8];
+    bf16x8_t va = *reinterpret_cast<const bf16x8_t*>(vfrag);
+    bf16x8_t vb = *reinterpret_cast<const bf16x8_t*>(vfrag + 16);
 #pragma unroll
     for (int d = 0; d < DB; ++d) {
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        uint2 w;
-        w.x = pack_bf16x2(oacc[d][4 * g4] * inv, oacc[d][4 * g4 + 1] * inv);
-        w.y = pack_bf16x2(oacc[d][4 * g4 + 2] * inv, oacc[d][4 * g4 + 3] * inv);
-        *reinterpret_cast<uint2*>(op + d * 32 + 8 * g4 + 4 * hg) = w;
+      for (int ks4 = 0; ks4 < 4; ks4 += 2) {
+        bf16x8_t na = va, nb = vb;
+        const int nd = (ks4 + 2 < 4) ? d : d + 1;
+        const int nk = (ks4 + 2 < 4) ? ks4 + 2 : 0;
+        if (nd < DB) {
+          na = *reinterpret_cast<const bf16x8_t*>(vfrag + nd * 32 * VS + nk * 16);
+          nb = *reinterpret_cast<const bf16x8_t*>(vfrag + nd * 32 * VS + (nk + 1) * 16);
+        }
+        oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pf[ks4], oacc[d], 0, 0, 0);
+        oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb, pf[ks4 + 1], oacc[d], 0, 0, 0);
+        va = na;
+        vb = nb;
       }
     }
-    if (p.lse != nullptr && hg == 0) {
-      const float lse2 = m_run + __log2f(l_tot);
-      p.lse[((int64_t)b * p.H + h) * p.Lq + qi] = lse2 / kLog2e;
+  };
+  auto publish = [&]() {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  };
+
+  TileIter cp;
+  cp.seek(p, wi.j0);
+  if constexpr (!PIPE) {
+    // double buffer: tile j+1 streams into LDS while tile j is computed
+    issue_k(0);
+    issue_v(0);
+    publish();
+    for (int j = 0; j < ntiles; ++j) {
+      if (j + 1 < ntiles) {
+        issue_k((j + 1) & 1);
+        issue_v((j + 1) & 1);
+      }
+      f32x16_t sacc[2];
+      bf16x8_t pf[4];
+      qk(j & 1, sacc);
+      softmax(sacc, cp.nvalid(), pf);
+      pv(j & 1, pf);
+      cp.next(p);
+      publish();
+    }
+  } else {
+    // K one tile ahead of V: tile j+1's Q.K^T is issued on the matrix cores
+    // before tile j's softmax, so the VALU work overlaps it.
+    f32x16_t s0[2], s1[2];
+    if (ntiles > 0) {
+      issue_k(0);
+      issue_v(0);
+      if (ntiles > 1) issue_k(1);
+      publish();
+      qk(0, s0);
+      __syncthreads();  // all waves are done with kbuf[0] before K2 replaces it
+    }
+    auto step = [&](int j, f32x16_t (&cur)[2], f32x16_t (&nxt)[2]) {
+      if (j + 2 < ntiles) issue_k(j & 1);
+      if (j + 1 < ntiles) {
+        issue_v((j + 1) & 1);
+        qk((j + 1) & 1, nxt);
+      }
+      bf16x8_t pf[4];
+      softmax(cur, cp.nvalid(), pf);
+      pv(j & 1, pf);
+      cp.next(p);
+      publish();
+    };
+    for (int j = 0; j < ntiles; j += 2) {
+      step(j, s0, s1);
+      if (j + 1 < ntiles) step(j + 1, s1, s0);
     }
   }
+
+  finish_tile<D>(p, wi, b, h, qt, oacc, m_run, pair_sum(l_run));
+}
+
+template <int D>
+int launch_combine(const FlashParams& p, hipStream_t st) {
+  if (p.split <= 1) return LTX_OK;
+  const int64_t tail = (int64_t)p.B * p.H * p.n_qtiles - p.n_full;
+  hipLaunchKernelGGL((flash_combine_kernel<D>), dim3((unsigned)tail), dim3(256), 0, st, p);
+  LTX_LAUNCH_CHECK("ltx_flash_attn_fwd (combine)");
+  return LTX_OK;
+}
+
+// Grid: whole q-tiles first, then the key-range pieces of the tail q-tiles.
+inline int64_t grid_blocks(const FlashParams& p) {
+  const int64_t nq = (int64_t)p.B * p.H * p.n_qtiles;
+  return p.n_full + (nq - p.n_full) * p.split;
+}
+
+template <int D, bool PIPE>
+int launch_flash_direct(const FlashParams& p, hipStream_t st) {
+  const int64_t nblocks = grid_blocks(p);
+  LTX_REQUIRE(nblocks <= 0x7FFFFFFF, "ltx_flash_attn_fwd: grid too large");
+  hipLaunchKernelGGL((flash_fwd_direct_kernel<D, PIPE>), dim3((unsigned)nblocks), dim3(256), 0, st, p);
+  LTX_LAUNCH_CHECK("ltx_flash_attn_fwd");
+  return launch_combine<D>(p, st);
 }
 
 template <int D, bool FP8, bool MASK>
 int launch_flash(const FlashParams& p, hipStream_t st) {
-  const int64_t nblocks = (int64_t)p.B * p.H * p.n_qtiles;
+  const int64_t nblocks = grid_blocks(p);
   LTX_REQUIRE(nblocks <= 0x7FFFFFFF, "ltx_flash_attn_fwd: grid too large");
   hipLaunchKernelGGL((flash_fwd_kernel<D, FP8, MASK>), dim3((unsigned)nblocks), dim3(256), 0, st, p);
   LTX_LAUNCH_CHECK("ltx_flash_attn_fwd");
-  return LTX_OK;
+  return launch_combine<D>(p, st);
 }
 
 }  // namespace ltx
 
 using namespace ltx;
 
+// Resident workgroups the device holds for this kernel (CUs x occupancy),
+// cached per device.
+template <typename K>
+int resident_slots(K kernel) {
+  static int cache[64][2];  // [device] -> {valid, slots}
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!cache[dev][0]) {
+    int cus = 0, occ = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, 256, 0) != hipSuccess) return 0;
+    cache[dev][1] = cus * (occ > 0 ? occ : 1);
+    cache[dev][0] = 1;
+  }
+  return cache[dev][1];
+}
+
+constexpr int kMaxSplit = 8;
+
+// Tail q-tiles (those past the last whole round of resident slots) and how
+// many key ranges each is cut into.  Only worth it when there is at least one
+// whole round (otherwise the grid is a single partial round and the extra
+// combine launch costs more than it saves) and each piece keeps >= 4 key
+// tiles.  Zero tail tiles: no split.
+inline void plan_split(int64_t nq, int ntiles, int slots, int64_t* n_full, int* split) {
+  *n_full = nq;
+  *split = 1;
+  if (slots <= 0 || nq < slots || nq % slots == 0) return;
+  const int64_t full = (nq / slots) * slots;
+  const int64_t tail = nq - full;
+  int sp = (int)(slots / (2 * tail));
+  if (sp > kMaxSplit) sp = kMaxSplit;
+  if (sp > ntiles / 4) sp = ntiles / 4;
+  if (sp < 2) return;
+  *n_full = full;
+  *split = sp;
+}
+
+inline int64_t workspace_bytes_for(int64_t tail, int split, int64_t D) {
+  return tail * split * kBM * (D + 2) * 4;
+}
+
+extern "C" int ltx_flash_attn_workspace_size(int64_t B, int64_t Lq, int64_t H, int64_t D,
+                                             int64_t* bytes) {
+  clear_error();
+  LTX_REQUIRE(bytes != nullptr && B >= 1 && H >= 1 && Lq >= 0 && (D == 64 || D == 128),
+              "ltx_flash_attn_workspace_size: bad arguments");
+  const int slots = resident_slots(flash_fwd_kernel<128, false, false>);
+  const int64_t nq = B * H * ((Lq + kBM - 1) / kBM);
+  int64_t n_full;
+  int split;
+  plan_split(nq, 1 << 30, slots, &n_full, &split);
+  *bytes = split > 1 ? workspace_bytes_for(nq - n_full, kMaxSplit, D) : 0;
+  return LTX_OK;
+}
+
 extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t H, int64_t D,
                                   int64_t q_bs, int64_t q_ls, int64_t q_hs, int64_t n_segments,
                                   const void* const* k_ptrs, const void* const* v_ptrs,
-                                  const int64_t* seg_lens, int64_t kv_bs, int64_t kv_ls,
-                                  int64_t kv_hs, int kv_dtype, const float* const* k_scales,
-                                  const float* const* v_scales, int64_t sc_bs, int64_t sc_hs,
-                                  int64_t frame_tokens, const float* key_mask, int64_t mask_bs,
-                                  void* out, int64_t o_bs, int64_t o_ls, int64_t o_hs, float* lse,
-                                  float scale, void* stream) {
+                                  const int64_t* seg_lens, int64_t k_bs, int64_t k_ls, int64_t k_hs,
+                                  int64_t v_bs, int64_t v_ls, int64_t v_hs, int64_t v_ds, int kv_dtype,
+                                  const float* const* k_scales, const float* const* v_scales,
+                                  int64_t sc_bs, int64_t sc_hs, int64_t frame_tokens,
+                                  const float* key_mask, int64_t mask_bs, void* out, int64_t o_bs,
+                                  int64_t o_ls, int64_t o_hs, float* lse, float scale,
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
   clear_error();
   LTX_REQUIRE(q && out, "ltx_flash_attn_fwd: null q/out");
   LTX_REQUIRE(D == 64 || D == 128, "ltx_flash_attn_fwd: head dim %lld unsupported (64 or 128)",
@@ -454,14 +930,25 @@ extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t 
   LTX_REQUIRE(kv_dtype == LTX_BF16 || kv_dtype == LTX_F8E4M3, "ltx_flash_attn_fwd: kv_dtype must be BF16 or F8E4M3");
   LTX_REQUIRE(n_segments == 0 || (k_ptrs && v_ptrs && seg_lens), "ltx_flash_attn_fwd: null segment arrays");
   const bool fp8 = kv_dtype == LTX_F8E4M3;
+  const bool vkey = v_ds != 1;  // key-major V
+  LTX_REQUIRE(!vkey || v_ls == 1, "ltx_flash_attn_fwd: V must be token-major (v_ds == 1) or key-major (v_ls == 1)");
+  LTX_REQUIRE(!vkey || (!fp8 && key_mask == nullptr),
+              "ltx_flash_attn_fwd: key-major V is bf16 without a key mask");
   const int64_t esz = fp8 ? 1 : 2;
   auto al = [](const void* ptr, uintptr_t a) { return ((uintptr_t)ptr % a) == 0; };
   LTX_REQUIRE(al(q, 16) && (q_bs * 2) % 16 == 0 && (q_ls * 2) % 16 == 0 && (q_hs * 2) % 16 == 0,
               "ltx_flash_attn_fwd: q rows must be 16-byte aligned");
   LTX_REQUIRE(al(out, 8) && (o_bs * 2) % 8 == 0 && (o_ls * 2) % 8 == 0 && (o_hs * 2) % 8 == 0,
               "ltx_flash_attn_fwd: out rows must be 8-byte aligned");
-  LTX_REQUIRE((kv_bs * esz) % 16 == 0 && (kv_ls * esz) % 16 == 0 && (kv_hs * esz) % 16 == 0,
-              "ltx_flash_attn_fwd: kv strides must keep 16-byte rows");
+  LTX_REQUIRE((k_bs * esz) % 16 == 0 && (k_ls * esz) % 16 == 0 && (k_hs * esz) % 16 == 0,
+              "ltx_flash_attn_fwd: K strides must keep 16-byte rows");
+  if (vkey)
+    LTX_REQUIRE((v_bs * 2) % 16 == 0 && (v_hs * 2) % 16 == 0 && (v_ds * 2) % 16 == 0 &&
+                    v_ds * D * 2 < ((int64_t)1 << 31),
+                "ltx_flash_attn_fwd: key-major V strides must keep 16-byte rows");
+  else
+    LTX_REQUIRE(v_bs == k_bs && v_ls == k_ls && v_hs == k_hs,
+                "ltx_flash_attn_fwd: token-major V must share K's strides");
 
   FlashParams p{};
   p.q = (const uint16_t*)q;
@@ -470,7 +957,8 @@ extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t 
   p.mask = key_mask;
   p.q_bs = q_bs; p.q_ls = q_ls; p.q_hs = q_hs;
   p.o_bs = o_bs; p.o_ls = o_ls; p.o_hs = o_hs;
-  p.kv_bs = kv_bs; p.kv_ls = kv_ls; p.kv_hs = kv_hs;
+  p.kv_bs = k_bs; p.kv_ls = k_ls; p.kv_hs = k_hs;
+  p.v_bs = v_bs; p.v_hs = v_hs; p.v_ds = v_ds;
   p.sc_bs = sc_bs; p.sc_hs = sc_hs;
   p.mask_bs = mask_bs;
   p.B = (int)B; p.H = (int)H; p.Lq = (int)Lq;
@@ -480,6 +968,7 @@ extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t 
   // drop empty segments
   int n = 0;
   p.seg_start[0] = 0;
+  p.tile_start[0] = 0;
   for (int64_t i = 0; i < n_segments; ++i) {
     LTX_REQUIRE(seg_lens[i] >= 0, "ltx_flash_attn_fwd: negative segment length");
     if (seg_lens[i] == 0) continue;
@@ -506,14 +995,39 @@ extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t 
   p.n_seg = n;
   p.Lk = p.seg_start[n];
   if (key_mask) LTX_REQUIRE(!fp8, "ltx_flash_attn_fwd: key mask with fp8 KV is not built");
-  LTX_REQUIRE(kv_ls * esz * kBN < (int64_t)1 << 31 && kv_ls >= D,
-              "ltx_flash_attn_fwd: kv token stride %lld out of range", (long long)kv_ls);
+  LTX_REQUIRE(k_ls * esz * kBN < (int64_t)1 << 31 && k_ls >= D,
+              "ltx_flash_attn_fwd: kv token stride %lld out of range", (long long)k_ls);
   p.n_qtiles = (int)((Lq + kBM - 1) / kBM);
   if (Lq == 0) return LTX_OK;
+  LTX_REQUIRE(n > 0, "ltx_flash_attn_fwd: no keys (Lk == 0)");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (n == 0) {
-    // no keys: softmax over an empty set; SDPA returns NaN rows, we define zeros
-    LTX_REQUIRE(false, "ltx_flash_attn_fwd: no keys (Lk == 0)");
+  // balanced tail (needs a workspace; without one every q-tile runs whole)
+  {
+    const int64_t nq = (int64_t)B * H * p.n_qtiles;
+    LTX_REQUIRE(nq <= 0x7FFFFFFF, "ltx_flash_attn_fwd: grid too large");
+    int64_t n_full = nq;
+    int split = 1;
+    if (workspace != nullptr) {
+      const int slots = vkey ? resident_slots(flash_fwd_direct_kernel<128, false>)
+                             : resident_slots(flash_fwd_kernel<128, false, false>);
+      plan_split(nq, p.tile_start[n], slots, &n_full, &split);
+      if (split > 1 && workspace_bytes_for(nq - n_full, split, D) > workspace_bytes) {
+        n_full = nq;
+        split = 1;
+      }
+    }
+    p.n_full = (int)n_full;
+    p.split = split;
+    if (split > 1) {
+      LTX_REQUIRE(al(workspace, 256), "ltx_flash_attn_fwd: workspace must be 256-byte aligned");
+      const int64_t tail = nq - n_full;
+      p.part_ml = static_cast<float*>(workspace);
+      p.part_o = p.part_ml + tail * split * kBM * 2;
+    }
+  }
+  if (vkey) {
+    if (D == 128) return launch_flash_direct<128, false>(p, st);
+    return launch_flash_direct<64, false>(p, st);
   }
   if (D == 128) {
     if (fp8) return launch_flash<128, true, false>(p, st);

@@ -17,10 +17,8 @@ __global__ void kv_copy_kernel(const TS* __restrict__ src, int64_t s_bs, int64_t
                                uint16_t* __restrict__ dst, int64_t d_bs, int64_t d_ls, int64_t d_hs,
                                int64_t L, int H, int D) {
   const int cpr = D / 8;  // 8 elements per chunk
-  const int64_t total = (int64_t)gridDim.y * L * H * cpr;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= L * H * cpr) return;
-  (void)total;
   const int b = blockIdx.y;
   const int c = (int)(gid % cpr);
   const int64_t lh = gid / cpr;
@@ -108,6 +106,56 @@ __global__ void __launch_bounds__(256) kv_quant_kernel(
   }
 }
 
+// Key-major append: a 64-token x D tile of one (b, h) goes through LDS so both
+// the token-major reads and the key-major writes are 16-byte vector accesses.
+template <typename TS, int D>
+__global__ void __launch_bounds__(256) kv_transpose_kernel(
+    const TS* __restrict__ src, int64_t s_bs, int64_t s_ls, int64_t s_hs, uint16_t* __restrict__ dst,
+    int64_t d_bs, int64_t d_hs, int64_t d_ds, int64_t L) {
+  constexpr int TT = 64;        // tokens per tile
+  constexpr int RS = D + 2;     // LDS row stride (elements): column reads spread over banks
+  __shared__ uint16_t tile[TT * RS];
+  const int64_t l0 = (int64_t)blockIdx.x * TT;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int rows = (int)((L - l0) < TT ? (L - l0) : TT);
+  constexpr int CPR = D / 8;
+  for (int idx = threadIdx.x; idx < TT * CPR; idx += blockDim.x) {
+    const int r = idx / CPR, c = idx % CPR;
+    if (r >= rows) continue;
+    const TS* sp = src + b * s_bs + (l0 + r) * s_ls + h * s_hs + c * 8;
+    uint32_t w[4];
+    if constexpr (sizeof(TS) == 2) {
+      const uint4 v = *reinterpret_cast<const uint4*>(sp);
+      w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else {
+      const float4 a = reinterpret_cast<const float4*>(sp)[0];
+      const float4 bb = reinterpret_cast<const float4*>(sp)[1];
+      w[0] = pack_bf16x2(a.x, a.y); w[1] = pack_bf16x2(a.z, a.w);
+      w[2] = pack_bf16x2(bb.x, bb.y); w[3] = pack_bf16x2(bb.z, bb.w);
+    }
+    uint32_t* tp = reinterpret_cast<uint32_t*>(&tile[r * RS + c * 8]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tp[i] = w[i];
+  }
+  __syncthreads();
+  // write: thread -> (d, 8-token chunk)
+  for (int idx = threadIdx.x; idx < D * (TT / 8); idx += blockDim.x) {
+    const int d = idx / (TT / 8), ch = idx % (TT / 8);
+    const int t0 = ch * 8;
+    if (t0 >= rows) continue;
+    uint16_t* dp = dst + b * d_bs + h * d_hs + d * d_ds + l0 + t0;
+    if (t0 + 8 <= rows) {
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = (uint32_t)tile[(t0 + 2 * i) * RS + d] | ((uint32_t)tile[(t0 + 2 * i + 1) * RS + d] << 16);
+      *reinterpret_cast<uint4*>(dp) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+      for (int i = 0; t0 + i < rows; ++i) dp[i] = tile[(t0 + i) * RS + d];
+    }
+  }
+}
+
 struct SpanTable {
   int64_t src_start[LTX_MAX_SEGMENTS];
   int64_t dst_start[LTX_MAX_SEGMENTS + 1];
@@ -140,13 +188,14 @@ using namespace ltx;
 
 extern "C" int ltx_kv_append(int src_dtype, int dst_dtype, int64_t B, int64_t L, int64_t H,
                              int64_t D, const void* src, int64_t s_bs, int64_t s_ls, int64_t s_hs,
-                             void* dst, int64_t d_bs, int64_t d_ls, int64_t d_hs, float* scales,
-                             int64_t sc_bs, int64_t sc_hs, int64_t frame_tokens, void* stream) {
+                             void* dst, int64_t d_bs, int64_t d_ls, int64_t d_hs, int64_t d_ds,
+                             float* scales, int64_t sc_bs, int64_t sc_hs, int64_t frame_tokens,
+                             void* stream) {
   clear_error();
   LTX_REQUIRE(src_dtype == LTX_BF16 || src_dtype == LTX_F32, "ltx_kv_append: src_dtype must be BF16 or F32");
   LTX_REQUIRE(dst_dtype == LTX_BF16 || dst_dtype == LTX_F8E4M3,
               "ltx_kv_append: dst_dtype must be BF16 or F8E4M3");
-  LTX_REQUIRE(B >= 1 && B <= 65535 && L >= 0 && H >= 1 && D >= 8 && D % 8 == 0,
+  LTX_REQUIRE(B >= 1 && B <= 65535 && L >= 0 && H >= 1 && H <= 65535 && D >= 8 && D % 8 == 0,
               "ltx_kv_append: bad shape");
   LTX_REQUIRE(src && dst, "ltx_kv_append: null pointer");
   const int64_t ssz = src_dtype == LTX_BF16 ? 2 : 4;
@@ -154,11 +203,31 @@ extern "C" int ltx_kv_append(int src_dtype, int dst_dtype, int64_t B, int64_t L,
   LTX_REQUIRE(((uintptr_t)src % 16) == 0 && (s_bs * ssz) % 16 == 0 && (s_ls * ssz) % 16 == 0 &&
                   (s_hs * ssz) % 16 == 0,
               "ltx_kv_append: src must be 16-byte aligned per row");
+  if (L == 0) return LTX_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (d_ds != 1) {
+    LTX_REQUIRE(d_ls == 1 && dst_dtype == LTX_BF16, "ltx_kv_append: dst must be token-major (d_ds == 1) "
+                "or bf16 key-major (d_ls == 1)");
+    LTX_REQUIRE(D == 64 || D == 128, "ltx_kv_append: key-major append supports D in {64, 128}");
+    LTX_REQUIRE(((uintptr_t)dst % 16) == 0 && (d_bs * 2) % 16 == 0 && (d_hs * 2) % 16 == 0 &&
+                    (d_ds * 2) % 16 == 0,
+                "ltx_kv_append: key-major dst must start on a 16-byte boundary (8-slot aligned)");
+    const dim3 grid((unsigned)ceil_div(L, 64), (unsigned)H, (unsigned)B);
+#define LTX_TRANSPOSE(TS, DD)                                                                     \
+  hipLaunchKernelGGL((kv_transpose_kernel<TS, DD>), grid, dim3(256), 0, st, (const TS*)src, s_bs, s_ls, \
+                     s_hs, (uint16_t*)dst, d_bs, d_hs, d_ds, L)
+    if (src_dtype == LTX_BF16) {
+      if (D == 128) LTX_TRANSPOSE(uint16_t, 128); else LTX_TRANSPOSE(uint16_t, 64);
+    } else {
+      if (D == 128) LTX_TRANSPOSE(float, 128); else LTX_TRANSPOSE(float, 64);
+    }
+#undef LTX_TRANSPOSE
+    LTX_LAUNCH_CHECK("ltx_kv_append");
+    return LTX_OK;
+  }
   LTX_REQUIRE(((uintptr_t)dst % 8) == 0 && (d_bs * dsz) % 8 == 0 && (d_ls * dsz) % 8 == 0 &&
                   (d_hs * dsz) % 8 == 0,
               "ltx_kv_append: dst must be 8-byte aligned per row");
-  if (L == 0) return LTX_OK;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (dst_dtype == LTX_BF16) {
     LTX_REQUIRE(((uintptr_t)dst % 16) == 0 && (d_bs * 2) % 16 == 0 && (d_ls * 2) % 16 == 0 &&
                     (d_hs * 2) % 16 == 0,

@@ -47,9 +47,12 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   return __builtin_bit_cast(uint16_t, b);
 }
 
-// Two float32 -> packed bf16x2 (low half = a).
+// Two float32 -> packed bf16x2 (low half = a), one v_cvt_pk_bf16_f32.
+typedef __bf16 ltx_bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float ltx_f32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+  const ltx_f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, ltx_bf16x2_t));
 }
 
 // OCP float8_e4m3fn encode: round to nearest even, saturating at +-448,

@@ -133,16 +133,20 @@ def qk_rmsnorm_rope(q_in: torch.Tensor, q_out: torch.Tensor, gamma_q: Optional[t
 
 def kv_append(src: torch.Tensor, dst: torch.Tensor, scales: Optional[torch.Tensor] = None,
               frame_tokens: int = 1) -> None:
-    """ltx_kv_append: src [B, L, H, D] -> dst [B, L, H, D] (bf16 copy or fp8 quantise).
+    """ltx_kv_append: src [B, L, H, D] -> dst [B, L, H, D] view.
 
-    For fp8, ``scales`` is a float32 [B, H, L/frame_tokens] view (any strides with
-    the frame index contiguous)."""
+    A token-major dst (head dim contiguous) is a bf16 copy or an fp8 quantise
+    (``scales`` float32 [B, H, L/frame_tokens], frame index contiguous); a
+    key-major dst (token stride 1, the arena's V layout) is a bf16 transpose."""
     _need_gpu(src, dst, scales)
     if src.dim() != 4 or dst.shape != src.shape:
         raise ValueError(f"kv_append: shapes {tuple(src.shape)} vs {tuple(dst.shape)}")
-    if src.stride(3) != 1 or dst.stride(3) != 1:
-        raise ValueError("kv_append: head dim must be contiguous")
+    if src.stride(3) != 1:
+        raise ValueError("kv_append: src head dim must be contiguous")
     B, L, H, D = src.shape
+    key_major = dst.stride(3) != 1
+    if key_major and (dst.stride(1) != 1 or _code(dst) != N.BF16):
+        raise ValueError("kv_append: dst must be token-major or bf16 key-major")
     sc_bs = sc_hs = 0
     if _code(dst) == N.F8E4M3:
         if scales is None or scales.dtype != torch.float32:
@@ -153,8 +157,8 @@ def kv_append(src: torch.Tensor, dst: torch.Tensor, scales: Optional[torch.Tenso
         sc_bs, sc_hs = scales.stride(0), scales.stride(1)
     N.call("ltx_kv_append", _code(src), _code(dst), B, L, H, D, src.data_ptr(),
            src.stride(0), src.stride(1), src.stride(2), dst.data_ptr(), dst.stride(0),
-           dst.stride(1), dst.stride(2), _ptr(scales), sc_bs, sc_hs, int(frame_tokens),
-           _stream(src))
+           dst.stride(1), dst.stride(2), dst.stride(3), _ptr(scales), sc_bs, sc_hs,
+           int(frame_tokens), _stream(src))
 
 
 def kv_gather(src: torch.Tensor, dst: torch.Tensor, spans: Sequence[Tuple[int, int]]) -> None:
@@ -178,6 +182,29 @@ def kv_gather(src: torch.Tensor, dst: torch.Tensor, spans: Sequence[Tuple[int, i
            src.stride(1), src.stride(2), dst.data_ptr(), dst.stride(0), dst.stride(1),
            dst.stride(2), len(spans), ctypes.cast(starts, ctypes.c_void_p),
            ctypes.cast(lens, ctypes.c_void_p), _stream(src))
+
+
+_WS_SIZE: dict = {}
+_WS: dict = {}
+
+
+def _flash_workspace(q: torch.Tensor, B: int, Lq: int, H: int, D: int):
+    """Device workspace for the balanced-tail split (partial results), one per
+    (device, stream) so overlapping launches never share one; grown on demand."""
+    key = (q.device.index, B, Lq, H, D)
+    need = _WS_SIZE.get(key)
+    if need is None:
+        out = ctypes.c_int64(0)
+        N.call("ltx_flash_attn_workspace_size", B, Lq, H, D, ctypes.byref(out))
+        need = _WS_SIZE[key] = int(out.value)
+    if need == 0:
+        return None, 0
+    skey = (q.device.index, _stream(q))
+    ws = _WS.get(skey)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(need, dtype=torch.uint8, device=q.device)
+        _WS[skey] = ws
+    return ws, ws.numel()
 
 
 class KVSegment:
@@ -204,22 +231,26 @@ def flash_attn(q: torch.Tensor, segments: List[KVSegment], out: torch.Tensor,
         raise ValueError("flash_attn: no keys")
     if len(segs) > N.MAX_SEGMENTS:
         raise ValueError(f"flash_attn: {len(segs)} segments > {N.MAX_SEGMENTS}")
-    k0 = segs[0].k
-    kv_code = _code(k0)
-    strides = None
+    kv_code = _code(segs[0].k)
+    kst = vst = None
     lk = 0
     for s in segs:
-        for t in (s.k, s.v):
+        for t, which in ((s.k, "k"), (s.v, "v")):
             _need_gpu(t)
             if t.dim() != 4 or t.shape[0] != B or t.shape[2] != H or t.shape[3] != D:
                 raise ValueError(f"flash_attn: segment {tuple(t.shape)} vs q {tuple(q.shape)}")
-            if _code(t) != kv_code or t.stride(3) != 1:
-                raise ValueError("flash_attn: segments must share dtype and have contiguous D")
-            st = (t.stride(0), t.stride(1), t.stride(2))
-            if strides is None:
-                strides = st
-            elif st != strides:
-                raise ValueError("flash_attn: all K/V segments must share (b, l, h) strides")
+            if _code(t) != kv_code:
+                raise ValueError("flash_attn: segments must share one dtype")
+        if s.k.stride(3) != 1:
+            raise ValueError("flash_attn: K head dim must be contiguous")
+        if s.v.stride(3) != 1 and s.v.stride(1) != 1:
+            raise ValueError("flash_attn: V must be token-major or key-major")
+        ks = (s.k.stride(0), s.k.stride(1), s.k.stride(2))
+        vs = (s.v.stride(0), s.v.stride(1), s.v.stride(2), s.v.stride(3))
+        if kst is None:
+            kst, vst = ks, vs
+        elif ks != kst or vs != vst:
+            raise ValueError("flash_attn: all K/V segments must share strides")
         if s.v.shape[1] != s.k.shape[1]:
             raise ValueError("flash_attn: k/v segment lengths differ")
         lk += s.k.shape[1]
@@ -246,6 +277,7 @@ def flash_attn(q: torch.Tensor, segments: List[KVSegment], out: torch.Tensor,
         mask_bs = 0 if key_mask.shape[0] == 1 else key_mask.stride(0)
     if lse is not None and (lse.dtype != torch.float32 or lse.shape != (B, H, Lq) or not lse.is_contiguous()):
         raise ValueError("flash_attn: lse must be contiguous float32 [B, H, Lq]")
+    ws, ws_bytes = _flash_workspace(q, B, Lq, H, D)
     kp = N.ptr_array([s.k.data_ptr() for s in segs])
     vp = N.ptr_array([s.v.data_ptr() for s in segs])
     lens = N.i64_array([s.k.shape[1] for s in segs])
@@ -253,8 +285,10 @@ def flash_attn(q: torch.Tensor, segments: List[KVSegment], out: torch.Tensor,
     vsp = N.ptr_array([s.v_scales.data_ptr() for s in segs]) if fp8 else None
     N.call("ltx_flash_attn_fwd", q.data_ptr(), B, Lq, H, D, q.stride(0), q.stride(1), q.stride(2),
            len(segs), ctypes.cast(kp, ctypes.c_void_p), ctypes.cast(vp, ctypes.c_void_p),
-           ctypes.cast(lens, ctypes.c_void_p), strides[0], strides[1], strides[2], kv_code,
+           ctypes.cast(lens, ctypes.c_void_p), kst[0], kst[1], kst[2], vst[0], vst[1], vst[2], vst[3],
+           kv_code,
            ctypes.cast(ksp, ctypes.c_void_p) if fp8 else None,
            ctypes.cast(vsp, ctypes.c_void_p) if fp8 else None, sc_bs, sc_hs,
            int(frame_tokens), _ptr(key_mask), mask_bs, out.data_ptr(), out.stride(0), out.stride(1),
-           out.stride(2), _ptr(lse), float(scale) if scale is not None else 0.0, _stream(q))
+           out.stride(2), _ptr(lse), float(scale) if scale is not None else 0.0, _ptr(ws), ws_bytes,
+           _stream(q))

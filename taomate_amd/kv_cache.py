@@ -20,8 +20,11 @@ re-concatenating.  Here every (layer, attention kind) owns one preallocated
   cache, a denoise-step cache) still covers it.  Liveness is tracked with
   weak references, so dropping the last reference to a view -- e.g. restoring
   the pre-block snapshot before the next denoise step -- frees its slots.
+* bf16 arenas keep K token-major [B, slots, H, D] and V key-major
+  [B, H, D, slots] (the attention kernel loads V^T tiles straight into LDS);
+  appends start on 8-slot boundaries.
 * fp8-e4m3 arenas store codes plus one float32 scale per (batch, head, frame)
-  of ``frame_tokens`` slots; spans are frame aligned.
+  of ``frame_tokens`` slots (both token-major); spans are frame aligned.
 """
 from __future__ import annotations
 
@@ -62,17 +65,27 @@ class KVArena:
                  name: str = ""):
         if kv_dtype not in ("bf16", "fp8"):
             raise ValueError(f"kv_dtype must be 'bf16' or 'fp8', got {kv_dtype!r}")
-        self.B, self.cap, self.H, self.D = int(batch), int(capacity), int(heads), int(dim_head)
+        self.B, self.H, self.D = int(batch), int(heads), int(dim_head)
+        # whole 8-slot groups: key-major V is read in 8-token chunks
+        self.cap = -(-int(capacity) // 8) * 8
         self.kv_dtype = kv_dtype
         self.fp8 = kv_dtype == "fp8"
         self.frame_tokens = int(frame_tokens) if self.fp8 else 1
-        if self.fp8 and self.cap % self.frame_tokens:
+        if self.fp8 and int(capacity) % self.frame_tokens:
             raise ValueError("fp8 arena capacity must be a whole number of frames")
         self.name = name
         self.device = torch.device(device)
         store = torch.uint8 if self.fp8 else torch.bfloat16
         self.k = torch.empty(self.B, self.cap, self.H, self.D, dtype=store, device=self.device)
-        self.v = torch.empty_like(self.k)
+        if self.fp8:
+            self.v = torch.empty_like(self.k)
+        else:
+            # bf16 V is stored key-major, [B, H, D, slots]: the attention kernel
+            # streams V^T tiles straight into LDS; self.v is its [B, slots, H, D]
+            # view.  Zero-filled: the kernel reads a span's last 8-slot group
+            # whole, so never-written slots must hold finite values.
+            self.v_store = torch.zeros(self.B, self.H, self.D, self.cap, dtype=store, device=self.device)
+            self.v = self.v_store.permute(0, 3, 1, 2)
         if self.fp8:
             nf = self.cap // self.frame_tokens
             self.k_scales = torch.ones(self.B, self.H, nf, dtype=torch.float32, device=self.device)
@@ -101,12 +114,18 @@ class KVArena:
                 out.append([a, b])
         return [(a, b) for a, b in out]
 
+    @property
+    def align(self) -> int:
+        """Slot alignment of appends: whole frames for fp8 (one scale per frame),
+        8 slots for bf16 (16-byte rows of the key-major V store)."""
+        return self.frame_tokens if self.fp8 else 8
+
     def alloc(self, n: int) -> int:
-        """First free slot range of n tokens (frame aligned for fp8) not covered
+        """First free slot range of n tokens (aligned to ``align``) not covered
         by any live view."""
         n = int(n)
-        al = self.frame_tokens
-        if n % al:
+        al = self.align
+        if self.fp8 and n % al:
             raise ValueError(f"append of {n} tokens is not a whole number of {al}-token frames")
         pos = 0
         for a, b in self.live_intervals() + [(self.cap, self.cap)]:
@@ -211,6 +230,11 @@ class KVSpanView:
         a = self.arena
         B, L, H, D = self.shape
         store = a.k if self.which == "k" else a.v
+        if self.which == "v" and not a.fp8:
+            # key-major V store: slice the spans of the [B, slots, H, D] view
+            if not L:
+                return torch.empty(B, 0, H, D, dtype=torch.bfloat16, device=a.device)
+            return torch.cat([store[:, s:s + n] for s, n in self.spans], dim=1).contiguous()
         dense = torch.empty(B, L, H, D, dtype=store.dtype, device=a.device)
         if L:
             kernels.kv_gather(store, dense, list(self.spans))

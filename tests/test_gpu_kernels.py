@@ -126,6 +126,21 @@ def test_kv_append_copy_bit_exact(dev):
     assert torch.count_nonzero(arena[:, :57]) == 0 and torch.count_nonzero(arena[:, 157:]) == 0
 
 
+@pytest.mark.parametrize("L,D,src_dt", [(100, 128, torch.bfloat16), (37, 64, torch.bfloat16),
+                                        (1152, 128, torch.float32)])
+def test_kv_append_key_major_bit_exact(dev, L, D, src_dt):
+    """Transposing append into a key-major [B, H, D, slots] store (the arena's V layout)."""
+    g = gen(12)
+    B, H = 2, 8
+    src = randn((B, L, H, D), g, src_dt).to(dev)
+    store = torch.zeros(B, H, D, -(-(L + 120) // 8) * 8, dtype=torch.bfloat16, device=dev)
+    view = store.permute(0, 3, 1, 2)                 # [B, slots, H, D], token stride 1
+    kernels.kv_append(src, view[:, 56:56 + L])
+    torch.cuda.synchronize()
+    assert torch.equal(view[:, 56:56 + L], src.to(torch.bfloat16))
+    assert torch.count_nonzero(store[..., :56]) == 0 and torch.count_nonzero(store[..., 56 + L:]) == 0
+
+
 @pytest.mark.parametrize("shape,frame", [((2, 1152, 32, 128), 384), ((1, 96, 8, 64), 96),
                                           ((1, 50, 32, 64), 25)])
 def test_kv_append_fp8_bit_exact(dev, shape, frame):
@@ -174,33 +189,40 @@ ATTN_CASES = [
 ]
 
 
+@pytest.mark.parametrize("vlayout", ["token", "key"])
 @pytest.mark.parametrize("case", ATTN_CASES, ids=lambda c: f"B{c[0]}q{c[1]}H{c[2]}D{c[3]}k{sum(c[4])}")
-def test_flash_attn_bf16_vs_fp32(dev, case):
+def test_flash_attn_bf16_vs_fp32(dev, case, vlayout):
+    """Segments scattered over one arena (gaps between spans).  token: V shares K's
+    [B, slots, H, D] layout (register-staged kernel); key: V in a key-major
+    [B, H, D, slots] store with 8-slot-aligned spans (direct-to-LDS kernel)."""
     B, Lq, H, D, lens = case
     g = gen(7)
     q = randn((B, Lq, H, D), g, torch.bfloat16)
     ks = [randn((B, n, H, D), g, torch.bfloat16) for n in lens]
     vs = [randn((B, n, H, D), g, torch.bfloat16) for n in lens]
-    # segments live in one arena with shared strides, at scattered slots
-    cap = sum(lens) + 64 * len(lens)
+    cap = -(-(sum(lens) + 64 * len(lens) + 64) // 8) * 8
     ka = torch.zeros(B, cap, H, D, dtype=torch.bfloat16, device=dev)
-    va = torch.zeros_like(ka)
+    if vlayout == "token":
+        va = torch.zeros_like(ka)
+    else:
+        va = torch.zeros(B, H, D, cap, dtype=torch.bfloat16, device=dev).permute(0, 3, 1, 2)
     segs, pos = [], 0
     for kk, vv in zip(ks, vs):
         n = kk.shape[1]
         ka[:, pos:pos + n] = kk.to(dev)
         va[:, pos:pos + n] = vv.to(dev)
         segs.append(KVSegment(ka[:, pos:pos + n], va[:, pos:pos + n]))
-        pos += n + 37  # gaps between spans
+        pos += n + 37
+        pos = -(-pos // 8) * 8   # spans start on 8-slot boundaries
     out = torch.empty(B, Lq, H, D, dtype=torch.bfloat16, device=dev)
     lse = torch.empty(B, H, Lq, dtype=torch.float32, device=dev)
     kernels.flash_attn(q.to(dev), segs, out, lse=lse)
     torch.cuda.synchronize()
     K, V = torch.cat(ks, 1), torch.cat(vs, 1)
     ref = _ref_attn(q, K, V)
-    assert_bf16_close(out, ref, f"attn {case}")
-    s = torch.einsum("bqhd,bkhd->bhqk", q.float(), K.float()) / math.sqrt(D)
-    assert (lse.cpu() - torch.logsumexp(s, -1)).abs().max().item() < 1e-2
+    assert_bf16_close(out, ref, f"attn {case} {vlayout}")
+    s_ = torch.einsum("bqhd,bkhd->bhqk", q.float(), K.float()) / math.sqrt(D)
+    assert (lse.cpu() - torch.logsumexp(s_, -1)).abs().max().item() < 1e-2
 
 
 def test_flash_attn_key_mask(dev):

@@ -1,0 +1,222 @@
+"""GPU parity of the drop-in attention surface against the fp32 CPU oracle:
+attention_with_cache over an arena cache (anchor | memory | window | current),
+the audio / cross-modal / text-cross attentions, and the streaming loop."""
+import gc
+import math
+
+import pytest
+import torch
+
+import taomate_amd as T
+from oracle import attention as OA
+from oracle import rope as OR
+
+from .helpers import BF16_MAX_ABS, BF16_MEAN_ABS, assert_bf16_close, cosine, diff_stats
+
+pytestmark = pytest.mark.gpu
+
+
+def make_layer(dev, d, H, Dh, seed, context_dim=None, gate=False):
+    """Seeded weights ~N(0, 0.02^2), zero biases, unit norm weights; the module
+    in bf16 on the GPU and the same values in fp32 for the oracle."""
+    g = torch.Generator().manual_seed(seed)
+    m = T.CausalLTXAttention(d, context_dim=context_dim, heads=H, dim_head=Dh, apply_gated_attention=gate)
+    with torch.no_grad():
+        lins = [m.to_q, m.to_k, m.to_v, m.to_out[0]] + ([m.to_gate_logits] if gate else [])
+        for lin in lins:
+            lin.weight.copy_(torch.randn(lin.weight.shape, generator=g) * 0.02)
+            lin.bias.zero_()
+    c = lambda t: t.detach().clone().float()
+    w = OA.AttnWeights(c(m.to_q.weight), c(m.to_q.bias), c(m.to_k.weight), c(m.to_k.bias),
+                       c(m.to_v.weight), c(m.to_v.bias), c(m.to_out[0].weight), c(m.to_out[0].bias),
+                       c(m.q_norm.weight), c(m.k_norm.weight), H, Dh,
+                       wg=c(m.to_gate_logits.weight) if gate else None,
+                       bg=c(m.to_gate_logits.bias) if gate else None)
+    return m.to(dev, torch.bfloat16), w
+
+
+def gpu_pe(dev, grid, dim, heads, start, B, audio=False):
+    return T.causal_precompute_freqs_cis(torch.tensor([list(grid)] * B), dim, start_frame=start, device=dev,
+                                         dtype=torch.bfloat16, num_attention_heads=heads, is_audio=audio)
+
+
+def ora_pe(grid, dim, heads, start, B, audio=False):
+    return OR.causal_precompute_freqs_cis(grid, dim, start_frame=start, num_attention_heads=heads, batch=B,
+                                          is_audio=audio)
+
+
+# (name, B, grid_h, grid_w, heads, dim_head, seed, kv_dtype)
+LAYERS = [
+    ("8x12grid_8x64", 1, 8, 12, 8, 64, 0, "bf16"),
+    ("16x24grid_32x128_B2", 2, 16, 24, 32, 128, 1, "bf16"),
+    ("16x24grid_32x128_B2_fp8", 2, 16, 24, 32, 128, 1, "fp8"),
+]
+# anchor frame 0 | memory frames | window frames | current chunk frames
+SEGS_SMALL = [("anchor", 0, 1), ("memory", 1, 1), ("window", 6, 4)]
+SEGS_FULL = [("anchor", 0, 1), ("memory", 1, 2), ("window", 6, 6)]
+
+
+_ORACLE = {}
+
+
+def _layer_reference(B, gh, gw, H, Dh, seed, w):
+    """fp32 oracle: prefill every segment at its absolute frames, then the chunk
+    over cat(cache, new).  Cached: the bf16 and fp8 cases share it."""
+    key = (B, gh, gw, H, Dh, seed)
+    if key not in _ORACLE:
+        d, hw = H * Dh, gh * gw
+        segs = SEGS_SMALL if H == 8 else SEGS_FULL
+        cur_f0, cur_nf = (10, 2) if H == 8 else (12, 3)
+        g = torch.Generator().manual_seed(seed + 100)
+        xs = [torch.randn(B, nf * hw, d, generator=g) for _, _, nf in segs]
+        xc = torch.randn(B, cur_nf * hw, d, generator=g)
+        ck = cv = None
+        for (nm, f0, nf), x in zip(segs, xs):
+            _, k, v = OA.attention_with_cache(w, x, None, ora_pe((nf, gh, gw), d, H, f0, B), None, None, None)
+            ck = k if ck is None else torch.cat([ck, k], 1)
+            cv = v if cv is None else torch.cat([cv, v], 1)
+        ref, ref_k, _ = OA.attention_with_cache(w, xc, None, ora_pe((cur_nf, gh, gw), d, H, cur_f0, B), None,
+                                                ck, cv)
+        _ORACLE[key] = (xs, xc, ref, ref_k)
+    return _ORACLE[key]
+
+
+@pytest.mark.parametrize("case", LAYERS, ids=[c[0] for c in LAYERS])
+def test_attention_with_cache_layer(dev, case):
+    name, B, gh, gw, H, Dh, seed, kvd = case
+    d = H * Dh
+    hw = gh * gw
+    segs = SEGS_SMALL if H == 8 else SEGS_FULL
+    cur_f0, cur_nf = (10, 2) if H == 8 else (12, 3)
+    attn, w = make_layer(dev, d, H, Dh, seed)
+    xs, xc, ref, ref_k = _layer_reference(B, gh, gw, H, Dh, seed, w)
+    # GPU: same calls through an arena cache
+    total = sum(nf for _, _, nf in segs) * hw + cur_nf * hw
+    spec = {"video_self": T.ArenaSpec(total, H, Dh, kvd, frame_tokens=hw)}
+    cache = T.init_kv_cache(1, B, spec, dev)
+    lay = cache.layers[0]
+    kc, vc = lay.video_self_k, lay.video_self_v
+    with torch.no_grad():
+        for (nm, f0, nf), x in zip(segs, xs):
+            _, nk, nv = T.attention_with_cache(attn, x.to(dev, torch.bfloat16), None,
+                                               gpu_pe(dev, (nf, gh, gw), d, H, f0, B), None, kc, vc)
+            kc, vc = T._cat_cache(kc, nk), T._cat_cache(vc, nv)
+        out, nk, nv = T.attention_with_cache(attn, xc.to(dev, torch.bfloat16), None,
+                                             gpu_pe(dev, (cur_nf, gh, gw), d, H, cur_f0, B), None, kc, vc)
+    torch.cuda.synchronize()
+    assert isinstance(nk, T.KVSpanView) and nk.shape == (B, cur_nf * hw, H, Dh)
+    assert kc.shape[1] == total - cur_nf * hw
+    if kvd == "bf16":
+        assert_bf16_close(out, ref, name)
+        assert cosine(nk.materialize(), ref_k) >= 0.9999
+    else:
+        assert diff_stats(out, ref)[0] <= BF16_MAX_ABS
+    c = cosine(out, ref)
+    assert c >= (0.999 if kvd == "fp8" else 0.9999), c
+
+
+def test_audio_and_cross_modal_attention(dev):
+    """Audio self-attention (75 queries over 600 cached + 75 new audio keys, 32 x 64,
+    1-D audio RoPE) and the A2V / V2A cross-modal attentions (1152 video tokens
+    <-> 75 audio tokens, projected to 32 x 64, 1-D cross RoPE)."""
+    B, Hh, Dh = 1, 32, 64
+    da, dv = 2048, 4096
+    g = torch.Generator().manual_seed(2)
+    # audio self: 24 cached blocks of 25 frames at latent frames 0..599, chunk at 600..674
+    attn, w = make_layer(dev, da, Hh, Dh, 20)
+    xa_old = torch.randn(B, 600, da, generator=g)
+    xa = torch.randn(B, 75, da, generator=g)
+    _, ck, cv = OA.attention_with_cache(w, xa_old, None, ora_pe((600,), da, Hh, 0, B, True), None, None, None)
+    ref, _, _ = OA.attention_with_cache(w, xa, None, ora_pe((75,), da, Hh, 600, B, True), None, ck, cv)
+    cache = T.init_kv_cache(1, B, {"audio_self": T.ArenaSpec(700, Hh, Dh)}, dev)
+    lay = cache.layers[0]
+    with torch.no_grad():
+        _, nk, nv = T.attention_with_cache(attn, xa_old.to(dev, torch.bfloat16), None,
+                                           gpu_pe(dev, (600,), da, Hh, 0, B, True), None,
+                                           lay.audio_self_k, lay.audio_self_v)
+        kc, vc = T._cat_cache(lay.audio_self_k, nk), T._cat_cache(lay.audio_self_v, nv)
+        out, _, _ = T.attention_with_cache(attn, xa.to(dev, torch.bfloat16), None,
+                                           gpu_pe(dev, (75,), da, Hh, 600, B, True), None, kc, vc)
+    assert_bf16_close(out, ref, "audio self")
+    assert cosine(out, ref) >= 0.9999
+
+    # cross-modal: video 3 frames x 384 tokens at frames 12..14, audio 75 frames at 100..174
+    xv = torch.randn(B, 1152, dv, generator=g)
+    xa = torch.randn(B, 75, da, generator=g)
+    vpe_o = [t.repeat_interleave(384, dim=2) for t in ora_pe((3,), 2048, Hh, 12, B)]
+    ape_o = ora_pe((75,), 2048, Hh, 100, B, True)
+    vpe_g = [t.repeat_interleave(384, dim=2).contiguous() for t in gpu_pe(dev, (3,), 2048, Hh, 12, B)]
+    ape_g = gpu_pe(dev, (75,), 2048, Hh, 100, B, True)
+    a2v, wa2v = make_layer(dev, dv, Hh, Dh, 21, context_dim=da)   # video queries, audio keys
+    v2a, wv2a = make_layer(dev, da, Hh, Dh, 22, context_dim=dv)   # audio queries, video keys
+    ref_a2v, _, _ = OA.attention_with_cache(wa2v, xv, xa, vpe_o, ape_o, None, None)
+    ref_v2a, _, _ = OA.attention_with_cache(wv2a, xa, xv, ape_o, vpe_o, None, None)
+    with torch.no_grad():
+        o_a2v, _, _ = T.attention_with_cache(a2v, xv.to(dev, torch.bfloat16), xa.to(dev, torch.bfloat16),
+                                             vpe_g, ape_g, None, None)
+        o_v2a, _, _ = T.attention_with_cache(v2a, xa.to(dev, torch.bfloat16), xv.to(dev, torch.bfloat16),
+                                             ape_g, vpe_g, None, None)
+    assert_bf16_close(o_a2v, ref_a2v, "A2V")
+    assert_bf16_close(o_v2a, ref_v2a, "V2A")
+    assert cosine(o_a2v, ref_a2v) >= 0.9999 and cosine(o_v2a, ref_v2a) >= 0.9999
+
+
+def test_text_cross_attention_with_padding_mask(dev):
+    """1152 video queries against 1024 text keys of dim 4096 (32 x 128), 20% of the
+    keys padding, through CausalLTXAttention.forward with the reference's
+    prepared additive mask (causal_model.py:551-562), gated output."""
+    B, H, Dh, d = 1, 32, 128, 4096
+    attn, w = make_layer(dev, d, H, Dh, 30, context_dim=d, gate=True)
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(B, 1152, d, generator=g)
+    ctx = torch.randn(B, 1024, d, generator=g)
+    keep = torch.ones(B, 1024, dtype=torch.int64)
+    keep[:, 819:] = 0
+    m = OA.prepare_attention_mask(keep, torch.bfloat16)
+    ref = OA.text_cross_attention(w, x, ctx, m.float())
+    with torch.no_grad():
+        out = attn(x.to(dev, torch.bfloat16), context=ctx.to(dev, torch.bfloat16), mask=m.to(dev))
+    assert_bf16_close(out, ref, "text cross")
+    assert cosine(out, ref) >= 0.9999
+
+
+def test_denoise_steps_do_not_commit(dev):
+    """Three denoise-step calls on a snapshot, then the commit: the committed cache
+    holds only the commit pass's keys, and step outputs equal the oracle's."""
+    B, H, Dh, d, hw = 1, 8, 64, 512, 96
+    attn, w = make_layer(dev, d, H, Dh, 40)
+    g = torch.Generator().manual_seed(41)
+    x0 = torch.randn(B, 4 * hw, d, generator=g)
+    pe0 = (ora_pe((4, 8, 12), d, H, 0, B), gpu_pe(dev, (4, 8, 12), d, H, 0, B))
+    pe1 = (ora_pe((3, 8, 12), d, H, 4, B), gpu_pe(dev, (3, 8, 12), d, H, 4, B))
+    _, ck, cv = OA.attention_with_cache(w, x0, None, pe0[0], None, None, None)
+    cache = T.init_kv_cache(1, B, {"video_self": T.ArenaSpec(10 * hw, H, Dh)}, dev)
+    lay = cache.layers[0]
+    with torch.no_grad():
+        _, nk, nv = T.attention_with_cache(attn, x0.to(dev, torch.bfloat16), None, pe0[1], None,
+                                           lay.video_self_k, lay.video_self_v)
+        cache.layers = [T.LayerKVCache(video_self_k=T._cat_cache(lay.video_self_k, nk),
+                                       video_self_v=T._cat_cache(lay.video_self_v, nv))]
+        del nk, nv, lay
+        snapshot = list(cache.layers)
+        for step in range(3):
+            cache.layers = list(snapshot)
+            xs = torch.randn(B, 3 * hw, d, generator=g)
+            ref, _, _ = OA.attention_with_cache(w, xs, None, pe1[0], None, ck, cv)
+            out, sk, sv = T.attention_with_cache(attn, xs.to(dev, torch.bfloat16), None, pe1[1], None,
+                                                 snapshot[0].video_self_k, snapshot[0].video_self_v)
+            cache.layers = [T.LayerKVCache(video_self_k=T._cat_cache(snapshot[0].video_self_k, sk),
+                                           video_self_v=T._cat_cache(snapshot[0].video_self_v, sv))]
+            assert_bf16_close(out, ref, f"step {step}")
+            del out, sk, sv
+        cache.layers = list(snapshot)
+        gc.collect()
+        xc = torch.randn(B, 3 * hw, d, generator=g)
+        _, rk, rv = OA.attention_with_cache(w, xc, None, pe1[0], None, ck, cv)
+        _, nk, nv = T.attention_with_cache(attn, xc.to(dev, torch.bfloat16), None, pe1[1], None,
+                                           snapshot[0].video_self_k, snapshot[0].video_self_v)
+        committed = T._cat_cache(snapshot[0].video_self_k, nk)
+    full = committed.materialize().float().cpu()
+    assert full.shape[1] == 7 * hw
+    assert cosine(full[:, 4 * hw:], rk) >= 0.9999
+    assert cosine(full[:, :4 * hw], ck) >= 0.9999

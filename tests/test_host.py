@@ -31,18 +31,21 @@ def test_blocks_match_oracle():
 
 def test_arena_alloc_first_fit_and_liveness():
     a = KVArena(1, 100, 1, 8, "cpu")
+    assert a.cap == 104                   # whole 8-slot groups
     v1 = KVSpanView(a, "k", [(a.alloc(30), 30)])
     assert v1.spans == ((0, 30),)
     v2 = KVSpanView(a, "k", [(a.alloc(30), 30)])
-    assert v2.spans == ((30, 30),)
+    assert v2.spans == ((32, 30),)        # bf16 appends start on 8-slot boundaries
     del v1
     gc.collect()
-    assert a.alloc(30) == 0          # freed slots are reused
-    assert a.alloc(31) == 60
-    v3 = KVSpanView(a, "k", [(60, 40)])
+    assert a.alloc(30) == 0               # freed slots are reused
+    assert a.alloc(33) == 64
+    v3 = KVSpanView(a, "k", [(64, 40)])
     with pytest.raises(T.KVArenaFull):
-        a.alloc(31)
+        a.alloc(33)
     assert a.alloc(30) == 0
+    assert torch.count_nonzero(a.v_store) == 0   # key-major V starts zeroed
+    assert a.v.shape == (1, 104, 1, 8) and a.v.stride(1) == 1
     del v2, v3
 
 
@@ -90,8 +93,8 @@ def test_streaming_eviction_plan_bit_exact(hw, n_blocks):
     logical token sequence after every commit with the oracle's plan."""
     plan = OC.streaming_plan(n_blocks, hw)
     per = hw[0] * hw[1]
-    cap_v = 4 * per + 2 * 3 * per + 3 * 3 * per
-    spec = {"video_self": T.ArenaSpec(cap_v, 1, 8), "audio_self": T.ArenaSpec(26 + 25 * 4, 1, 8)}
+    cap_v = 4 * per + 2 * 3 * per + 3 * 3 * per + 4 * 8   # + room for 8-slot alignment
+    spec = {"video_self": T.ArenaSpec(cap_v, 1, 8), "audio_self": T.ArenaSpec(26 + 25 * 4 + 4 * 8, 1, 8)}
     cache = T.init_kv_cache(1, 1, spec, "cpu")
     blocks = T.compute_av_blocks(4 + (n_blocks - 1) * 3, num_frame_per_block_first=4)[:n_blocks]
     segments = []
@@ -185,15 +188,15 @@ def test_abi_rejects_bad_arguments_without_a_gpu():
     rc = lib.ltx_rope_table(None, None, 1, None, 0, 3, 1, 1, 1, 0, 0, 20.0, 2048.0, 2048.0, 64, 1, 1, None)
     assert rc == -1 and b"null pointer" in lib.ltx_last_error()
     rc = lib.ltx_flash_attn_fwd(ctypes.c_void_p(16), 1, 1, 1, 96, 0, 0, 0, 0, None, None, None, 0, 0, 0,
-                                1, None, None, 0, 0, 0, None, 0, ctypes.c_void_p(16), 0, 0, 0, None,
-                                0.0, None)
+                                0, 0, 0, 1, 1, None, None, 0, 0, 0, None, 0, ctypes.c_void_p(16), 0, 0,
+                                0, None, 0.0, None, 0, None)
     assert rc == -1 and b"head dim" in lib.ltx_last_error()
     rc = lib.ltx_kv_gather(3, 1, 1, 8, None, 0, 0, 0, None, 0, 0, 0, 0, None, None, None)
     assert rc == -1
     with pytest.raises(_native.NativeCallError, match="n_segments"):
         _native.call("ltx_flash_attn_fwd", ctypes.c_void_p(16), 1, 1, 1, 128, 0, 0, 0, 17, None, None,
-                     None, 0, 0, 0, 1, None, None, 0, 0, 0, None, 0, ctypes.c_void_p(16), 0, 0, 0, None,
-                     0.0, None)
+                     None, 0, 0, 0, 0, 0, 0, 1, 1, None, None, 0, 0, 0, None, 0, ctypes.c_void_p(16), 0,
+                     0, 0, None, 0.0, None, 0, None)
 
 
 def test_kernels_refuse_cpu_tensors():

@@ -59,6 +59,24 @@ def append_bytes() -> float:
     return 2 * B * LQ * HD * 2  # V read + written
 
 
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "attention_b2_h32_d128_1152q_4608k_hbm_traffic.md")
+
+
+def measured_traffic(kv_dtype: str):
+    """HBM bytes per attention call (attention + combine kernels) for this
+    workload, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (line `traffic_bytes_per_call[<kv>]: N`); None when not profiled."""
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            for line in f:
+                key = f"traffic_bytes_per_call[{kv_dtype}]:"
+                if line.strip().startswith(key):
+                    return int(line.split(":", 1)[1].strip().strip("`"))
+    except OSError:
+        pass
+    return None
+
+
 def build_workload(dev, kv_dtype: str = "bf16"):
     from taomate_amd import kernels
     from taomate_amd.kv_cache import KVArena
@@ -137,7 +155,9 @@ def make_step(w):
 
 
 def time_region(fn, iters: int) -> float:
-    """Average ms per call over `iters` calls, HIP events on the launching stream."""
+    """Average ms per call over `iters` back-to-back calls, HIP events on the
+    launching stream (profiling aid; the reported figures come from the timed
+    step loop)."""
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -195,18 +215,29 @@ def cpu_baseline(seconds_budget: float = 20.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--kv", choices=["bf16", "fp8"], default="bf16")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--attn-only", action="store_true", help="loop only the attention kernel (profiling)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain 256 MiB device copy (scale reference for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs the hot path on one GPU; --gpus must be 1 "
               "(multi-GPU sharding is described, not run)", file=sys.stderr)
         sys.exit(2)
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        n = 64 * 1024 * 1024
+        x = torch.ones(n, device=dev)
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "launches": 3}))
+        return
     w = build_workload(dev, args.kv)
     step, attn, norm, append = make_step(w)
     if args.attn_only:
@@ -217,14 +248,32 @@ def main():
         return
     for _ in range(args.warmup):
         step()
+    # Timed region: K steps bracketed by synchronisations; HIP events on the
+    # launching stream split every step into its three parts, so each kernel's
+    # average duration is measured inside the same region as the step time.
+    st = torch.cuda.current_stream()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    e_start, e_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    ms_step = time_region(step, args.steps)
+    e_start.record(st)
+    for i in range(args.steps):
+        e = ev[i]
+        e[0].record(st)
+        norm()
+        e[1].record(st)
+        append()
+        e[2].record(st)
+        attn()
+        e[3].record(st)
+    e_end.record(st)
+    e_end.synchronize()
+    torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    # per-kernel averages on the same stream
-    ms_attn = time_region(attn, max(20, args.steps))
-    ms_norm = time_region(norm, max(20, args.steps))
-    ms_app = time_region(append, max(20, args.steps))
+    ms_step = e_start.elapsed_time(e_end) / args.steps
+    ms_norm = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
+    ms_app = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
+    ms_attn = sum(e[2].elapsed_time(e[3]) for e in ev) / args.steps
     kvb = 1 if args.kv == "fp8" else 2
     fl = attn_flops()
     ach = fl / (ms_attn * 1e-3) / 1e12
@@ -248,8 +297,10 @@ def main():
                    "kv_dtype": args.kv, "global_batch": B, "seq_len": LQ, "keys": LK,
                    "heads": H, "head_dim": D, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": ach, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": ach / PEAK_BF16_TFLOPS, "traffic": None,
-                     "kernel": "flash_fwd_kernel", "kernel_ms": ms_attn,
+                     "frac": ach / PEAK_BF16_TFLOPS, "traffic": measured_traffic(args.kv),
+                     "kernel": ("flash_fwd_direct_kernel<128> + flash_combine_kernel<128>" if args.kv == "bf16"
+                                else "flash_fwd_kernel<128, fp8> + flash_combine_kernel<128>"),
+                     "kernel_ms": ms_attn,
                      "algorithmic_flops": fl, "algorithmic_bytes": attn_bytes(kvb)},
         "attention_tflops": ach,
         "attention_query_tokens_per_s": B * LQ / (ms_attn * 1e-3),

@@ -247,38 +247,56 @@ __device__ __forceinline__ void finish_tile(const FlashParams& p, const WorkItem
   if (hg == 0) *reinterpret_cast<float2*>(p.part_ml + ((int64_t)w.piece * kBM + row) * 2) = make_float2(m_run, l_tot);
 }
 
-// Combines the `split` partial results of every tail q-tile: one workgroup per
-// tail q-tile, launched after the attention kernel on the same stream.
+constexpr int kMaxSplit = 8;  // key ranges a tail q-tile may be cut into
+
+// Combines the `split` partial results of every tail q-tile, launched after the
+// attention kernel on the same stream.  One thread per (query row, 4 output
+// columns): every piece's (max, sum) and O values are loaded up front, so each
+// thread waits for one round of loads.
 template <int D>
 __global__ void __launch_bounds__(256) flash_combine_kernel(const FlashParams p) {
-  const int tail = blockIdx.x;
+  constexpr int C4 = D / 4;             // float4 columns per row
+  constexpr int ROWS = 256 / C4;        // rows per workgroup
+  constexpr int WG_PER_TILE = kBM / ROWS;
+  const int tail = blockIdx.x / WG_PER_TILE;
+  const int r = (blockIdx.x % WG_PER_TILE) * ROWS + threadIdx.x / C4;
+  const int c4 = threadIdx.x % C4;
   const int qtile = p.n_full + tail;
   const int qt = qtile % p.n_qtiles;
   const int bh = qtile / p.n_qtiles;
   const int b = bh / p.H, h = bh % p.H;
-  const int first = tail * p.split;
-  for (int idx = threadIdx.x; idx < kBM * (D / 4); idx += blockDim.x) {
-    const int r = idx / (D / 4), c4 = idx % (D / 4);
-    const int q = qt * kBM + r;
-    if (q >= p.Lq) continue;
-    float mmax = -INFINITY;
-    for (int i = 0; i < p.split; ++i) mmax = fmaxf(mmax, p.part_ml[((int64_t)(first + i) * kBM + r) * 2]);
-    float lsum = 0.0f;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int i = 0; i < p.split; ++i) {
-      const float2 ml = *reinterpret_cast<const float2*>(p.part_ml + ((int64_t)(first + i) * kBM + r) * 2);
-      const float wgt = __builtin_amdgcn_exp2f(ml.x - mmax);
-      lsum += wgt * ml.y;
-      const float4 o = *reinterpret_cast<const float4*>(p.part_o + ((int64_t)(first + i) * kBM + r) * D + c4 * 4);
-      acc.x += wgt * o.x; acc.y += wgt * o.y; acc.z += wgt * o.z; acc.w += wgt * o.w;
+  const int q = qt * kBM + r;
+  if (q >= p.Lq) return;
+  const int64_t first = (int64_t)tail * p.split;
+  f32x2_t ml[kMaxSplit];
+  float4 o[kMaxSplit];
+#pragma unroll
+  for (int i = 0; i < kMaxSplit; ++i) {
+    if (i < p.split) {
+      ml[i] = *reinterpret_cast<const f32x2_t*>(p.part_ml + ((first + i) * kBM + r) * 2);
+      o[i] = *reinterpret_cast<const float4*>(p.part_o + ((first + i) * kBM + r) * D + c4 * 4);
     }
-    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-    uint2 v;
-    v.x = pack_bf16x2(acc.x * inv, acc.y * inv);
-    v.y = pack_bf16x2(acc.z * inv, acc.w * inv);
-    *reinterpret_cast<uint2*>(p.o + b * p.o_bs + (int64_t)q * p.o_ls + h * p.o_hs + c4 * 4) = v;
-    if (p.lse != nullptr && c4 == 0) p.lse[((int64_t)b * p.H + h) * p.Lq + q] = (mmax + __log2f(lsum)) / kLog2e;
   }
+  float mmax = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kMaxSplit; ++i)
+    if (i < p.split) mmax = fmaxf(mmax, ml[i][0]);
+  float lsum = 0.0f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int i = 0; i < kMaxSplit; ++i) {
+    if (i < p.split) {
+      const float wgt = ml[i][0] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml[i][0] - mmax);
+      lsum += wgt * ml[i][1];
+      acc.x += wgt * o[i].x; acc.y += wgt * o[i].y; acc.z += wgt * o[i].z; acc.w += wgt * o[i].w;
+    }
+  }
+  const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+  uint2 v;
+  v.x = pack_bf16x2(acc.x * inv, acc.y * inv);
+  v.y = pack_bf16x2(acc.z * inv, acc.w * inv);
+  *reinterpret_cast<uint2*>(p.o + b * p.o_bs + (int64_t)q * p.o_ls + h * p.o_hs + c4 * 4) = v;
+  if (p.lse != nullptr && c4 == 0) p.lse[((int64_t)b * p.H + h) * p.Lq + q] = (mmax + __log2f(lsum)) / kLog2e;
 }
 
 template <int D, bool FP8, bool MASK>
@@ -821,7 +839,8 @@ template <int D>
 int launch_combine(const FlashParams& p, hipStream_t st) {
   if (p.split <= 1) return LTX_OK;
   const int64_t tail = (int64_t)p.B * p.H * p.n_qtiles - p.n_full;
-  hipLaunchKernelGGL((flash_combine_kernel<D>), dim3((unsigned)tail), dim3(256), 0, st, p);
+  const int64_t wg_per_tile = kBM / (256 / (D / 4));
+  hipLaunchKernelGGL((flash_combine_kernel<D>), dim3((unsigned)(tail * wg_per_tile)), dim3(256), 0, st, p);
   LTX_LAUNCH_CHECK("ltx_flash_attn_fwd (combine)");
   return LTX_OK;
 }
@@ -871,7 +890,6 @@ int resident_slots(K kernel) {
   return cache[dev][1];
 }
 
-constexpr int kMaxSplit = 8;
 
 // Tail q-tiles (those past the last whole round of resident slots) and how
 // many key ranges each is cut into.  Only worth it when there is at least one

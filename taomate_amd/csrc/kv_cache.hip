@@ -7,6 +7,8 @@
 // the new tokens into their slots, eviction is slot bookkeeping on the host,
 // and gather is the optional physical compaction of the surviving spans.
 
+#include <type_traits>
+
 #include "ltx_common.h"
 
 namespace ltx {
@@ -40,14 +42,22 @@ __global__ void kv_copy_kernel(const TS* __restrict__ src, int64_t s_bs, int64_t
   }
 }
 
-// One workgroup per (frame, h, b): absmax over frame_tokens x D, then quantise.
-template <typename TS>
-__global__ void __launch_bounds__(256) kv_quant_kernel(
+// One workgroup of kQuantThreads per (frame, h, b): absmax over the frame's
+// frame_tokens x D values, then quantise.  Each thread keeps its first
+// kQuantRegs 8-value chunks in registers between the two passes, so frames of
+// up to kQuantThreads * kQuantRegs chunks are read from memory once; chunks
+// beyond that are read again in the second pass.
+constexpr int kQuantThreads = 1024;
+constexpr int kQuantRegs = 8;
+
+// CPR: 8-value chunks per row (D / 8) when known at compile time, 0 otherwise.
+template <typename TS, int CPR>
+__global__ void __launch_bounds__(kQuantThreads) kv_quant_kernel(
     const TS* __restrict__ src, int64_t s_bs, int64_t s_ls, int64_t s_hs, uint8_t* __restrict__ dst,
     int64_t d_bs, int64_t d_ls, int64_t d_hs, float* __restrict__ scales, int64_t sc_bs,
     int64_t sc_hs, int frame_tokens, int D) {
   const int f = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int cpr = D / 8;
+  const int cpr = CPR > 0 ? CPR : D / 8;
   const int n = frame_tokens * cpr;  // 8-element chunks in this (frame, head)
   const int64_t l0 = (int64_t)f * frame_tokens;
   const TS* sbase = src + b * s_bs + l0 * s_ls + h * s_hs;
@@ -71,38 +81,59 @@ __global__ void __launch_bounds__(256) kv_quant_kernel(
       v[4] = bb.x; v[5] = bb.y; v[6] = bb.z; v[7] = bb.w;
     }
   };
-
-  float amax = 0.0f;
-  for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
-    float v[8];
-    load8(idx, v);
+  auto store8 = [&](int idx, const float* v, float sc, float r) {
+    float q[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    for (int i = 0; i < 8; ++i) q[i] = quotient_for_e4m3(v[i], sc, r);
+    const uint32_t lo = pack4_e4m3(q[0], q[1], q[2], q[3]);
+    const uint32_t hi = pack4_e4m3(q[4], q[5], q[6], q[7]);
+    const int t = idx / cpr, c = idx % cpr;
+    *reinterpret_cast<uint2*>(dbase + (int64_t)t * d_ls + c * 8) = make_uint2(lo, hi);
+  };
+
+  float v[kQuantRegs][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kQuantRegs; ++i) {
+    const int idx = threadIdx.x + i * kQuantThreads;
+    if (idx < n) {
+      load8(idx, v[i]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[i][e]));
+    }
+  }
+  for (int idx = threadIdx.x + kQuantRegs * kQuantThreads; idx < n; idx += kQuantThreads) {
+    float t[8];
+    load8(idx, t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(t[e]));
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-  __shared__ float red[4];
+  constexpr int kWaves = kQuantThreads / 64;
+  __shared__ float red[kWaves];
   __shared__ float scale_s;
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
   __syncthreads();
   if (threadIdx.x == 0) {
-    float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float sc = m > 0.0f ? __fdiv_rn(m, 448.0f) : 1.0f;
+    float m = red[0];
+    for (int w = 1; w < kWaves; ++w) m = fmaxf(m, red[w]);
+    const float sc = m > 0.0f ? __fdiv_rn(m, 448.0f) : 1.0f;
     scale_s = sc;
     scales[b * sc_bs + h * sc_hs + f] = sc;
   }
   __syncthreads();
   const float sc = scale_s;
-  for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
-    float v[8];
-    load8(idx, v);
-    uint32_t lo = 0, hi = 0;
+  const float r = __fdiv_rn(1.0f, sc);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) lo |= f32_to_e4m3(__fdiv_rn(v[i], sc)) << (8 * i);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) hi |= f32_to_e4m3(__fdiv_rn(v[4 + i], sc)) << (8 * i);
-    const int t = idx / cpr, c = idx % cpr;
-    *reinterpret_cast<uint2*>(dbase + (int64_t)t * d_ls + c * 8) = make_uint2(lo, hi);
+  for (int i = 0; i < kQuantRegs; ++i) {
+    const int idx = threadIdx.x + i * kQuantThreads;
+    if (idx < n) store8(idx, v[i], sc, r);
+  }
+  for (int idx = threadIdx.x + kQuantRegs * kQuantThreads; idx < n; idx += kQuantThreads) {
+    float t[8];
+    load8(idx, t);
+    store8(idx, t, sc, r);
   }
 }
 
@@ -246,14 +277,24 @@ extern "C" int ltx_kv_append(int src_dtype, int dst_dtype, int64_t B, int64_t L,
                 "ltx_kv_append: L (%lld) must be a multiple of frame_tokens (%lld)", (long long)L,
                 (long long)frame_tokens);
     const dim3 grid((unsigned)(L / frame_tokens), (unsigned)H, (unsigned)B);
-    if (src_dtype == LTX_BF16)
-      hipLaunchKernelGGL(kv_quant_kernel<uint16_t>, grid, dim3(256), 0, st, (const uint16_t*)src, s_bs,
-                         s_ls, s_hs, (uint8_t*)dst, d_bs, d_ls, d_hs, scales, sc_bs, sc_hs,
-                         (int)frame_tokens, (int)D);
-    else
-      hipLaunchKernelGGL(kv_quant_kernel<float>, grid, dim3(256), 0, st, (const float*)src, s_bs, s_ls,
-                         s_hs, (uint8_t*)dst, d_bs, d_ls, d_hs, scales, sc_bs, sc_hs,
-                         (int)frame_tokens, (int)D);
+    auto launch = [&](auto tag, auto cpr) {
+      using TS = decltype(tag);
+      hipLaunchKernelGGL((kv_quant_kernel<TS, decltype(cpr)::value>), grid, dim3(kQuantThreads), 0, st,
+                         (const TS*)src, s_bs, s_ls, s_hs, (uint8_t*)dst, d_bs, d_ls, d_hs, scales,
+                         sc_bs, sc_hs, (int)frame_tokens, (int)D);
+    };
+    using C16 = std::integral_constant<int, 16>;
+    using C8 = std::integral_constant<int, 8>;
+    using C0 = std::integral_constant<int, 0>;
+    if (src_dtype == LTX_BF16) {
+      if (D == 128) launch(uint16_t{}, C16{});
+      else if (D == 64) launch(uint16_t{}, C8{});
+      else launch(uint16_t{}, C0{});
+    } else {
+      if (D == 128) launch(float{}, C16{});
+      else if (D == 64) launch(float{}, C8{});
+      else launch(float{}, C0{});
+    }
   }
   LTX_LAUNCH_CHECK("ltx_kv_append");
   return LTX_OK;

@@ -55,44 +55,30 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, ltx_bf16x2_t));
 }
 
-// OCP float8_e4m3fn encode: round to nearest even, saturating at +-448,
-// NaN -> 0x7F.  Written from the format definition (1 sign, 4 exponent bits
-// with bias 7, 3 mantissa bits, no infinities, S.1111.111 = NaN).
-__device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
-  uint32_t u = __float_as_uint(x);
-  uint32_t sign = (u >> 24) & 0x80u;
-  float a = fabsf(x);
-  if (!(a == a)) return 0x7Fu;             // NaN
-  if (a >= 448.0f) return sign | 0x7Eu;    // saturate
-  if (a < 0.015625f) {                     // below 2^-6: subnormal grid of 2^-9
-    // a / 2^-9 rounded to nearest even integer in [0, 8]; 8 is the smallest normal.
-    float m = __builtin_rintf(a * 512.0f);
-    return sign | (uint32_t)m;             // m == 8 encodes 2^-6 exactly (0x08)
-  }
-  uint32_t ua = __float_as_uint(a);
-  // keep 3 mantissa bits with round-to-nearest-even on the dropped 20 bits
-  uint32_t lsb = (ua >> 20) & 1u;
-  ua += 0x7FFFFu + lsb;
-  uint32_t e = (ua >> 23) - 127u + 7u;     // rebias (ua >= 2^-6 so e >= 1)
-  uint32_t m = (ua >> 20) & 7u;
-  uint32_t code = (e << 3) | m;
-  if (code > 0x7Eu) code = 0x7Eu;           // rounding carried past 448
-  return sign | code;
+// fl(x / sc) given r = fl(1 / sc).  fl(x * r) is within 3 ulp of fl(x / sc),
+// so both round to the same e4m3 value unless the quotient lies next to a
+// rounding midpoint of the e4m3 grid (low 20 mantissa bits near 0x80000) or in
+// the e4m3 subnormal range (below 2^-6); only those lanes pay for the exact
+// division.  The result is only meant for rounding to e4m3.
+__device__ __forceinline__ float quotient_for_e4m3(float x, float sc, float r) {
+  const float q = x * r;
+  const float a = fabsf(q);
+  const uint32_t low = __float_as_uint(a) & 0xFFFFFu;
+  if (a < 0.015625f || low - 0x7FFFCu <= 8u) return __fdiv_rn(x, sc);
+  return q;
 }
 
-// OCP float8_e4m3fn decode to float32 (exact).
-__device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
-  uint32_t sign = (c & 0x80u) << 24;
-  uint32_t e = (c >> 3) & 0xFu;
-  uint32_t m = c & 7u;
-  float v;
-  if (e == 0) {
-    v = (float)m * 0.001953125f;  // m * 2^-9
-  } else {
-    v = __uint_as_float(((e + 120u) << 23) | (m << 20));
-  }
-  if ((c & 0x7Fu) == 0x7Fu) v = __uint_as_float(0x7FC00000u);
-  return __uint_as_float(__float_as_uint(v) | sign);
+// Four float32 values -> four OCP e4m3fn codes (byte i = value i): clamp to
+// +-448, then the gfx950 converter rounds to nearest even.
+__device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d) {
+  const float m = 448.0f;
+  a = __builtin_amdgcn_fmed3f(a, -m, m);
+  b = __builtin_amdgcn_fmed3f(b, -m, m);
+  c = __builtin_amdgcn_fmed3f(c, -m, m);
+  d = __builtin_amdgcn_fmed3f(d, -m, m);
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
 }
 
 template <typename T>

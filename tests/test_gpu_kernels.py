@@ -157,6 +157,67 @@ def test_kv_append_fp8_bit_exact(dev, shape, frame):
     assert torch.equal(dst.cpu(), codes_ref)
 
 
+def _frames_to_src(frames, D=64):
+    """Pack 1-D float32 frames into a [1, n*F, 1, D] source, F tokens per frame."""
+    F = max(math.ceil(len(f) / D) for f in frames)
+    out = torch.zeros(len(frames), F * D, dtype=torch.float32)
+    for i, f in enumerate(frames):
+        out[i, :len(f)] = f
+    return out.view(1, len(frames) * F, 1, D), F
+
+
+def test_kv_append_fp8_rounding_ties(dev):
+    """Quotients exactly on, and one float32 ulp either side of, every e4m3
+    value and every midpoint between neighbours (ties go to even), subnormals
+    included; then the same grid scaled by awkward per-frame scales so x/scale
+    lands within a few ulp of midpoints."""
+    grid = sorted({OF.e4m3_value(c) for c in range(0x7F)})
+    g64 = torch.tensor(grid, dtype=torch.float64)
+    base = torch.cat([g64, (g64[1:] + g64[:-1]) / 2]).float()
+    inf = torch.tensor(float("inf"))
+    vals = torch.cat([base, torch.nextafter(base, inf), torch.nextafter(base, -inf)])
+    vals = vals.clamp(max=448.0)
+    vals[1::2] *= -1
+    frames = [torch.cat([vals, torch.tensor([448.0])])]           # scale exactly 1
+    gen_ = torch.Generator().manual_seed(11)
+    for m in (3.7, 0.0131, 1234.5, 1e-3, 7.0, 0.3):
+        sc = torch.tensor(m, dtype=torch.float32) / 448.0
+        t = base[base <= 440.0]
+        x = (t * sc).float()
+        # perturb by -3..3 ulp so quotients straddle the midpoints
+        k = torch.randint(-3, 4, x.shape, generator=gen_)
+        for _ in range(3):
+            x = torch.where(k > 0, torch.nextafter(x, inf), torch.where(k < 0, torch.nextafter(x, -inf), x))
+            k = k - k.sign()
+        x[1::2] *= -1
+        frames.append(torch.cat([x, torch.tensor([m], dtype=torch.float32)]))
+    src, F = _frames_to_src(frames)
+    codes_ref, sc_ref = OF.quantize_kv(src, F)
+    dst = torch.zeros(src.shape, dtype=torch.uint8, device=dev)
+    sc = torch.zeros(1, 1, len(frames), dtype=torch.float32, device=dev)
+    kernels.kv_append(src.to(dev), dst, sc, F)
+    torch.cuda.synchronize()
+    assert torch.equal(sc.cpu(), sc_ref)
+    assert torch.equal(dst.cpu(), codes_ref)
+
+
+def test_kv_append_fp8_many_scales(dev):
+    """16.7M bf16 values under per-head scales from 1e-3 to 1e3: every lane
+    of the reciprocal fast path and of the exact-division fallback agrees
+    with the float32 division of the reference quantiser."""
+    g = gen(12)
+    B, L, H, D, frame = 1, 4096, 32, 128, 512
+    mag = 10.0 ** (torch.rand(1, 1, H, 1, generator=g) * 6 - 3)
+    src = (torch.randn(B, L, H, D, generator=g) * mag).to(torch.bfloat16)
+    codes_ref, sc_ref = OF.quantize_kv(src.float(), frame)
+    dst = torch.empty(B, L, H, D, dtype=torch.uint8, device=dev)
+    sc = torch.empty(B, H, L // frame, dtype=torch.float32, device=dev)
+    kernels.kv_append(src.to(dev), dst, sc, frame)
+    torch.cuda.synchronize()
+    assert torch.equal(sc.cpu(), sc_ref)
+    assert torch.equal(dst.cpu(), codes_ref)
+
+
 def test_kv_gather_bit_exact(dev):
     g = gen(6)
     B, L, H, D = 2, 500, 8, 64

@@ -97,3 +97,38 @@ def test_quantize_kv_scales_and_error_bound():
     s_tok = sc.permute(0, 2, 1).repeat_interleave(384, 1).unsqueeze(-1)
     err = (y - x).abs()
     assert torch.all(err <= x.abs() * 2 ** -4 + s_tok * 2 ** -10 + 1e-12)
+
+
+def test_fp8_reciprocal_fast_path_argument():
+    """The fp8 quantiser multiplies by r = fl(1/scale) and divides exactly only
+    when fl(x*r) lies within 4 ulp of an e4m3 rounding midpoint (low 20
+    mantissa bits in [0x7FFFC, 0x80004]) or below 2^-6.  Emulated here in
+    float32 on quotients placed at and around every midpoint under awkward
+    scales: the e4m3 codes equal those of fl(x/scale)."""
+    g = torch.Generator().manual_seed(3)
+    grid = sorted({OF.e4m3_value(c) for c in range(0x7F)})
+    g64 = torch.tensor(grid, dtype=torch.float64)
+    mids = ((g64[1:] + g64[:-1]) / 2).float()
+    inf = torch.tensor(float("inf"))
+    for m in torch.rand(200, generator=g) * 1e3 + 1e-4:
+        sc = (m.float() / 448.0).float()
+        x = (mids * sc).float()
+        for _ in range(int(torch.randint(0, 6, (1,), generator=g))):
+            x = torch.nextafter(x, inf if torch.rand(1, generator=g) < 0.5 else -inf)
+        x = torch.cat([x, -x, torch.randn(4096, generator=g) * m])
+        q = x / sc
+        r = (torch.tensor(1.0) / sc).float()
+        qf = x * r
+        a = qf.abs()
+        low = a.view(torch.int32) & 0xFFFFF
+        near = (a < 2.0 ** -6) | ((low >= 0x7FFFC) & (low <= 0x80004))
+        qf = torch.where(near, q, qf)
+        c_exact = q.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+        c_fast = qf.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+        assert torch.equal(c_exact, c_fast)
+    # a window that is too narrow is caught (planted mistake)
+    sc = torch.tensor(3.7 / 448.0, dtype=torch.float32)
+    x = (mids * sc).float()
+    q, qf = x / sc, x * (torch.tensor(1.0) / sc).float()
+    assert not torch.equal(q.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8),
+                           qf.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8))

@@ -554,36 +554,86 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(const FlashParams p) 
   finish_tile<D>(p, wi, b, h, qt, oacc, m_run, pair_sum(l_run));
 }
 
-// ---------------------------------------------------------------------------
-// Direct-to-LDS variant (bf16; K token-major, V key-major in HBM).
-//
-// gfx950 buffer loads can write 16 bytes per lane straight into LDS (lane L of
-// an instruction lands at base + 16*L).  Each instruction therefore covers 64
-// consecutive 16-byte LDS chunks of a padded tile: a K row is 16 data chunks
-// plus 1 pad chunk (the same 272-byte rows as the register-staged kernel), a
-// V^T row (one head-dim channel, 64 keys) 8 data chunks plus 1 pad.  Lanes
-// that fall on a pad chunk re-read a valid chunk.  The K-row order swap and
-// the V transpose both happen in the address each lane reads from, so no
-// registers and no VALU work go into staging.  V must be stored key-major
-// (the KV arena's V layout); a segment's last 8-token chunk is read whole,
-// its keys past the segment end are masked out of the softmax.
-// ---------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-template <int D, bool PIPE>
-__global__ void __launch_bounds__(256, 2) flash_fwd_direct_kernel(const FlashParams p) {
+// ---------------------------------------------------------------------------
+// Software-pipelined direct kernel (bf16; K token-major, V key-major in HBM).
+//
+// K and V^T tiles go HBM -> LDS with buffer_load ... lds (gfx950 writes 16
+// bytes per lane straight into LDS: lane L of an instruction lands at base +
+// 16*L), so no VGPRs and no VALU work go into staging.  Each instruction
+// covers 64 consecutive 16-byte LDS chunks of a padded tile: a K row is 16
+// data chunks plus 1 pad chunk (272-byte rows), a V^T row (one head-dim
+// channel, 64 keys) 8 data chunks plus 1 pad; lanes that fall on a pad chunk
+// re-read a valid chunk.  The K-row order swap and the V transpose both
+// happen in the address each lane reads from.  V must be stored key-major
+// (the KV arena's V layout); a segment's last 8-token chunk is read whole and
+// its keys past the segment end are masked out of the softmax.
+//
+// The per-tile vector work is cut down and moved under the matrix cores:
+//
+// * P = 2^(S*c - m) (c = scale*log2 e) is one v_fma and one v_exp per score:
+//   no tile maximum is taken on the common path.
+// * The row sum comes from v_dot2c_f32_bf16 over the packed bf16 P (two keys
+//   per instruction) and doubles as the overflow check: m is not raised every
+//   tile.  While the per-lane sum of a tile stays at or below 2^16, every P
+//   of that tile is at most 2^16, which fp32 sums and bf16 P carry as exactly
+//   as P <= 1.  When a lane's sum goes above it, the tile maximum is taken
+//   and m, O and l are rescaled before P is redone (the online normaliser of
+//   Milakov & Gimelshein 2018).  The first tile sets m from its own maximum,
+//   so the sums never underflow.  Logits stay fp32-exact (Q is not rescaled).
+// * Pipeline: iteration j computes O += V(j-1)^T P(j-1) on the matrix cores
+//   while the vector unit turns S(j) into P(j), then S(j+1) = K(j+1) Q^T.
+//   K is loaded two tiles ahead and V one tile ahead of their use; one
+//   barrier per tile frees the buffers read in the previous iteration.
+// ---------------------------------------------------------------------------
+
+// One operand (K or V) of the concatenated segments, walked tile by tile with
+// wave-uniform state: the segment, the keys it has left from the current
+// tile on, and the byte address of the current tile's first key (segment base
+// + the (b, h) offset + the rows already passed).  Total keys < 2^31 (checked
+// on the host).
+struct KeyStream {
+  int s, rem;
+  const char* ptr;
+  __device__ __forceinline__ void enter(const void* const* base, int64_t head, const FlashParams& p, int seg) {
+    s = seg;
+    rem = (int)(p.seg_start[seg + 1] - p.seg_start[seg]);
+    ptr = reinterpret_cast<const char*>(base[seg]) + head;
+  }
+  __device__ __forceinline__ void seek(const void* const* base, int64_t head, int64_t tile_bytes,
+                                       const FlashParams& p, int j) {
+    int seg = 0;
+    for (int i = 1; i < p.n_seg; ++i) seg = (j >= p.tile_start[i]) ? i : seg;
+    enter(base, head, p, seg);
+    const int t = j - p.tile_start[seg];
+    rem -= t * kBN;
+    ptr += t * tile_bytes;
+  }
+  __device__ __forceinline__ void next(const void* const* base, int64_t head, int64_t tile_bytes,
+                                       const FlashParams& p) {
+    rem -= kBN;
+    ptr += tile_bytes;
+    if (rem <= 0 && s + 1 < p.n_seg) enter(base, head, p, s + 1);
+  }
+  __device__ __forceinline__ int nvalid() const { return rem < kBN ? rem : kBN; }
+};
+
+template <int D>
+__global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParams p) {
   constexpr int BM = kBM, BN = kBN;
-  constexpr int NKC = D / 8;                 // data chunks per K row
-  constexpr int KS = D + 8;                  // padded K row (elements)
-  constexpr int VS = BN + 8;                 // padded V^T row (elements)
+  constexpr int NKC = D / 8;
+  constexpr int KS = D + 8;
+  constexpr int VS = BN + 8;
   constexpr int KBUF = BN * KS;
   constexpr int VBUF = D * VS;
-  constexpr int KINS = BN * (NKC + 1) / 64;  // load instructions per K tile
-  constexpr int VINS = D * 9 / 64;           // load instructions per V^T tile
-  constexpr int KSLOT = (KINS + 3) / 4;      // per wave
+  constexpr int KINS = BN * (NKC + 1) / 64;
+  constexpr int VINS = D * 9 / 64;
+  constexpr int KSLOT = (KINS + 3) / 4;
   constexpr int VSLOT = (VINS + 3) / 4;
   constexpr int DB = D / 32;
   constexpr int QS = D / 16;
+  constexpr float kOver = 65536.0f;  // largest per-lane tile sum kept without raising m
   static_assert(BN * (NKC + 1) % 64 == 0 && D * 9 % 64 == 0, "tile does not split into whole instructions");
 
   __shared__ __attribute__((aligned(16))) uint16_t kbuf[2][KBUF];
@@ -593,11 +643,13 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_direct_kernel(const FlashPar
   const int qt = wi.qtile % p.n_qtiles;
   const int bh = wi.qtile / p.n_qtiles;
   const int b = bh / p.H, h = bh % p.H;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) & 3;
+  const int lane = threadIdx.x & 63;
   const int li = lane & 31, hg = lane >> 5;
   const int qi = qt * BM + wave * 32 + li;
   const int ntiles = wi.j1 - wi.j0;
 
+  // ---- Q^T fragments, resident for the whole key loop ----
   bf16x8_t qf[QS];
   {
     const bool ok = qi < p.Lq;
@@ -609,13 +661,9 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_direct_kernel(const FlashPar
     }
   }
 
-  // Per-lane source offsets (bytes from the tile's first key) of every load
-  // instruction this wave issues; loop invariant.  krow/vchk keep the row and
-  // chunk so the last, partial tile of a segment can clamp them.
+  // ---- per-lane load offsets (bytes from a tile's first key), loop invariant ----
   const int row_bytes = (int)(p.kv_ls * 2);
-  int koff[KSLOT], voff[VSLOT];
-  // (row, chunk) of this lane's chunk in instruction slot i, pad chunks mapped
-  // onto a data chunk; recomputed only for a segment's partial last tile
+  const int vrow_bytes = (int)(p.v_ds * 2);
   auto kpos = [&](int i, int& r, int& c) {
     const int pch = (wave + 4 * i) * 64 + lane;
     r = sig(pch / (NKC + 1));
@@ -629,6 +677,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_direct_kernel(const FlashPar
     c = pch % 9;
     c = c < 8 ? c : 0;
   };
+  int koff[KSLOT], voff[VSLOT];
 #pragma unroll
   for (int i = 0; i < KSLOT; ++i) {
     int r, c;
@@ -639,141 +688,152 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_direct_kernel(const FlashPar
   for (int i = 0; i < VSLOT; ++i) {
     int d, c;
     vpos(i, d, c);
-    voff[i] = (int)(d * p.v_ds * 2) + c * 16;
+    voff[i] = d * vrow_bytes + c * 16;
   }
 
-  const int64_t k_off = b * p.kv_bs + h * p.kv_hs;
-  const int64_t v_off = b * p.v_bs + h * p.v_hs;
-  TileIter kit, vit;
-  kit.seek(p, wi.j0);
-  vit.seek(p, wi.j0);
+  const int64_t k_head = (b * p.kv_bs + h * p.kv_hs) * 2;
+  const int64_t v_head = (b * p.v_bs + h * p.v_hs) * 2;
+  const int64_t k_tile = (int64_t)BN * p.kv_ls * 2;
+  constexpr int64_t v_tile = BN * 2;
+  KeyStream kit, vit;
+  kit.seek(p.k_ptr, k_head, k_tile, p, wi.j0);
+  vit.seek(p.v_ptr, v_head, v_tile, p, wi.j0);
+  // LDS address of this wave's first load slot in a buffer; the empty asm
+  // keeps the compiler from holding every (buffer, slot) address in its own
+  // scalar register across the loop (they cost one s_add each instead)
+  auto lds_slot0 = [&](uint16_t* buf0) {
+    uint32_t a = (uint32_t)(uintptr_t)(lds_ptr_t)(buf0 + wave * 512);
+    asm volatile("" : "+s"(a));
+    return a;
+  };
   auto issue_k = [&](int buf) {
-    const char* base = reinterpret_cast<const char*>(kit.k) + (k_off + kit.row0 * p.kv_ls) * 2;
-    const auto rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, 0x7FFFFFFF, 0x00020000);
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc((void*)kit.ptr, (short)0, 0x7FFFFFFF, 0x00020000);
     const int nv = kit.nvalid();
+    const uint32_t l0 = lds_slot0(kbuf[buf]);
+    if (nv == BN) {
 #pragma unroll
-    for (int i = 0; i < KSLOT; ++i) {
-      const int q = wave + 4 * i;
-      if (q < KINS) {
-        int off = koff[i];
-        if (nv < BN) {
+      for (int i = 0; i < KSLOT; ++i)
+        if (wave + 4 * i < KINS) {
+          const int off = koff[i];  // a local: an array element as the offset operand trips clang's host pass
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(uintptr_t)(l0 + i * 4096), 16, off, 0, 0, 0);
+        }
+    } else {
+      // a segment's last, partial tile: rows past its end re-read its last row
+#pragma unroll
+      for (int i = 0; i < KSLOT; ++i)
+        if (wave + 4 * i < KINS) {
           int r, c;
           kpos(i, r, c);
-          off = min(r, nv - 1) * row_bytes + c * 16;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(uintptr_t)(l0 + i * 4096), 16,
+                                                   min(r, nv - 1) * row_bytes + c * 16, 0, 0, 0);
         }
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(&kbuf[buf][q * 512]), 16, off, 0, 0, 0);
-      }
     }
-    kit.next(p);
+    kit.next(p.k_ptr, k_head, k_tile, p);
   };
   auto issue_v = [&](int buf) {
-    const char* base = reinterpret_cast<const char*>(vit.v) + (v_off + vit.row0) * 2;
-    const auto rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, 0x7FFFFFFF, 0x00020000);
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc((void*)vit.ptr, (short)0, 0x7FFFFFFF, 0x00020000);
     const int nv = vit.nvalid();
+    const uint32_t l0 = lds_slot0(vbuf[buf]);
+    if (nv == BN) {
 #pragma unroll
-    for (int i = 0; i < VSLOT; ++i) {
-      const int q = wave + 4 * i;
-      if (q < VINS) {
-        int off = voff[i];
-        if (nv < BN) {
+      for (int i = 0; i < VSLOT; ++i)
+        if (wave + 4 * i < VINS) {
+          const int off = voff[i];
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(uintptr_t)(l0 + i * 4096), 16, off, 0, 0, 0);
+        }
+    } else {
+      // 8-key chunks past the segment's last one re-read it
+#pragma unroll
+      for (int i = 0; i < VSLOT; ++i)
+        if (wave + 4 * i < VINS) {
           int d, c;
           vpos(i, d, c);
-          off = (int)(d * p.v_ds * 2) + min(c, (nv + 7) / 8 - 1) * 16;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(uintptr_t)(l0 + i * 4096), 16,
+                                                   d * vrow_bytes + min(c, (nv + 7) / 8 - 1) * 16, 0, 0, 0);
         }
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(&vbuf[buf][q * 512]), 16, off, 0, 0, 0);
-      }
     }
-    vit.next(p);
-  };
-  auto qk = [&](int buf, f32x16_t (&acc)[2]) {
-    acc[0] = f32x16_t{};
-    acc[1] = f32x16_t{};
-    const uint16_t* kfrag = &kbuf[buf][li * KS + hg * 8];
-    bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(kfrag);
-    bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(kfrag + 32 * KS);
-#pragma unroll
-    for (int s = 0; s < QS; ++s) {
-      bf16x8_t n0 = a0, n1 = a1;
-      if (s + 1 < QS) {
-        n0 = *reinterpret_cast<const bf16x8_t*>(kfrag + (s + 1) * 16);
-        n1 = *reinterpret_cast<const bf16x8_t*>(kfrag + 32 * KS + (s + 1) * 16);
-      }
-      acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[s], acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[s], acc[1], 0, 0, 0);
-      a0 = n0;
-      a1 = n1;
-    }
+    vit.next(p.v_ptr, v_head, v_tile, p);
   };
 
   f32x16_t oacc[DB];
 #pragma unroll
   for (int d = 0; d < DB; ++d) oacc[d] = f32x16_t{};
-  constexpr float kLazy = 8.0f;
   const float c = p.scale_log2;
-  float m_run = -INFINITY;
-  float l_run = 0.0f;
+  float m_run = -INFINITY;  // per query, base-2 logit units
+  float l_run = 0.0f;       // this lane's share of the row sum
 
-  // softmax of one tile's S^T accumulators into bf16 P fragments
-  auto softmax = [&](f32x16_t (&sacc)[2], int nvalid, bf16x8_t (&pf)[4]) {
-    if (nvalid < BN) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kb * 32 + 16 * (r >> 3) + 8 * hg + (r & 7);
-          if (key >= nvalid) sacc[kb][r] = -INFINITY;
-        }
-    }
-    float mt = sacc[0][0];
+  // keys past a partial tile's valid count drop out of the softmax (the
+  // lane's key is kb*32 + 16*(r/8) + 8*hg + r%8: compare its constant part
+  // with one per-lane limit so no key index is kept in registers)
+  auto mask_tail = [&](f32x16_t (&s)[2], int nvalid) {
+    const int lim = nvalid - 8 * hg;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[kb][r]);
-    const float m_tile = pair_max(mt) * c;
-    if (__builtin_amdgcn_ballot_w64(m_tile > m_run + kLazy)) {
-      const float m_new = fmaxf(m_run, m_tile);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-      m_run = m_new;
-      l_run *= alpha;
-#pragma unroll
-      for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
-    }
-    const float neg_m = -m_run;
-    float psum = 0.0f;
-#pragma unroll
-    for (int ks4 = 0; ks4 < 4; ++ks4) {
-      const int kb = ks4 >> 1, t = ks4 & 1;
-      uint32_t w[4];
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][8 * t + e], c, neg_m));
-        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][8 * t + e + 1], c, neg_m));
-        psum += p0 + p1;
-        w[e >> 1] = pack_bf16x2(p0, p1);
-      }
-      pf[ks4] = __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
-    }
-    l_run += psum;
+      for (int r = 0; r < 16; ++r)
+        if (kb * 32 + 16 * (r >> 3) + (r & 7) >= lim) s[kb][r] = -INFINITY;
   };
-  auto pv = [&](int buf, const bf16x8_t (&pf)[4]) {
-    const uint16_t* vfrag = &vbuf[buf][li * VS + hg * 8];
-    bf16x8_t va = *reinterpret_cast<const bf16x8_t*>(vfrag);
-    bf16x8_t vb = *reinterpret_cast<const bf16x8_t*>(vfrag + 16);
+  // largest base-2 logit of a tile for this lane's query (c > 0)
+  auto tile_max = [&](const f32x16_t (&s)[2]) {
+    float mt = s[0][0];
 #pragma unroll
-    for (int d = 0; d < DB; ++d) {
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int ks4 = 0; ks4 < 4; ks4 += 2) {
-        bf16x8_t na = va, nb = vb;
-        const int nd = (ks4 + 2 < 4) ? d : d + 1;
-        const int nk = (ks4 + 2 < 4) ? ks4 + 2 : 0;
-        if (nd < DB) {
-          na = *reinterpret_cast<const bf16x8_t*>(vfrag + nd * 32 * VS + nk * 16);
-          nb = *reinterpret_cast<const bf16x8_t*>(vfrag + nd * 32 * VS + (nk + 1) * 16);
-        }
-        oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pf[ks4], oacc[d], 0, 0, 0);
-        oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb, pf[ks4 + 1], oacc[d], 0, 0, 0);
+      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][r]);
+    return pair_max(mt) * c;
+  };
+  const ltx_bf16x2_t ones = __builtin_bit_cast(ltx_bf16x2_t, 0x3F803F80u);  // bf16 pair (1, 1)
+  // P = 2^(S*c - m) packed to bf16 pairs (pw[i] holds scores 2i, 2i+1 in
+  // accumulator order), and the per-lane sums of the two key blocks
+  auto exp_pack = [&](const f32x16_t (&s)[2], uint32_t (&pw)[16], float& ps0, float& ps1) {
+    const float neg_m = -m_run;
+    ps0 = 0.0f;
+    ps1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i += 2) {
+      const int kb = i >> 4, r = i & 15;
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], c, neg_m));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r + 1], c, neg_m));
+      pw[i >> 1] = pack_bf16x2(p0, p1);
+      float& ps = kb == 0 ? ps0 : ps1;
+      ps = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(ltx_bf16x2_t, pw[i >> 1]), ones, ps, false);
+    }
+  };
+  // S = K Q^T from kbuf[buf]
+  auto qk = [&](int buf, f32x16_t (&s)[2]) {
+    const f32x16_t zero = f32x16_t{};
+    const uint16_t* kf = &kbuf[buf][li * KS + hg * 8];
+    bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(kf);
+    bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(kf + 32 * KS);
+#pragma unroll
+    for (int k = 0; k < QS; ++k) {
+      bf16x8_t n0 = a0, n1 = a1;
+      if (k + 1 < QS) {
+        n0 = *reinterpret_cast<const bf16x8_t*>(kf + (k + 1) * 16);
+        n1 = *reinterpret_cast<const bf16x8_t*>(kf + 32 * KS + (k + 1) * 16);
+      }
+      s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[k], k == 0 ? zero : s[0], 0, 0, 0);
+      s[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[k], k == 0 ? zero : s[1], 0, 0, 0);
+      a0 = n0;
+      a1 = n1;
+    }
+  };
+  // O^T += V^T P^T from vbuf[buf]; consecutive MFMAs use different accumulators
+  auto pv = [&](int buf, const uint32_t (&pw)[16]) {
+    const uint16_t* vf = &vbuf[buf][li * VS + hg * 8];
+    bf16x8_t va = *reinterpret_cast<const bf16x8_t*>(vf);
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4) {
+      const bf16x8_t pf =
+          __builtin_bit_cast(bf16x8_t, make_uint4(pw[4 * k4], pw[4 * k4 + 1], pw[4 * k4 + 2], pw[4 * k4 + 3]));
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+        bf16x8_t na = va;
+        const int nd = d + 1 < DB ? d + 1 : 0;
+        const int nk = d + 1 < DB ? k4 : k4 + 1;
+        if (nk < 4) na = *reinterpret_cast<const bf16x8_t*>(vf + nd * 32 * VS + nk * 16);
+        oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pf, oacc[d], 0, 0, 0);
         va = na;
-        vb = nb;
       }
     }
   };
@@ -782,54 +842,63 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_direct_kernel(const FlashPar
     __syncthreads();
   };
 
-  TileIter cp;
-  cp.seek(p, wi.j0);
-  if constexpr (!PIPE) {
-    // double buffer: tile j+1 streams into LDS while tile j is computed
+  if (ntiles > 0) {
+    f32x16_t s[2];
+    uint32_t pa[16], pb[16];  // P(j) of even / odd j
+    // ---- prologue: S(0) sets m from its own maximum; P(0); S(1) ----
     issue_k(0);
+    if (ntiles > 1) issue_k(1);
+    const int nv0 = vit.nvalid();  // valid keys of tile 0 (the V stream is at tile j before V(j) is issued)
     issue_v(0);
     publish();
-    for (int j = 0; j < ntiles; ++j) {
-      if (j + 1 < ntiles) {
-        issue_k((j + 1) & 1);
-        issue_v((j + 1) & 1);
-      }
-      f32x16_t sacc[2];
-      bf16x8_t pf[4];
-      qk(j & 1, sacc);
-      softmax(sacc, cp.nvalid(), pf);
-      pv(j & 1, pf);
-      cp.next(p);
-      publish();
+    {
+      qk(0, s);
+      if (nv0 < BN) mask_tail(s, nv0);
+      m_run = tile_max(s);
+      float ps0, ps1;
+      exp_pack(s, pa, ps0, ps1);
+      l_run = ps0 + ps1;
+      if (ntiles > 1) qk(1, s);
     }
-  } else {
-    // K one tile ahead of V: tile j+1's Q.K^T is issued on the matrix cores
-    // before tile j's softmax, so the VALU work overlaps it.
-    f32x16_t s0[2], s1[2];
-    if (ntiles > 0) {
-      issue_k(0);
-      issue_v(0);
-      if (ntiles > 1) issue_k(1);
-      publish();
-      qk(0, s0);
-      __syncthreads();  // all waves are done with kbuf[0] before K2 replaces it
+    if (ntiles > 2) {
+      __syncthreads();  // every wave is done with K(0)
+      issue_k(0);       // K(2)
     }
-    auto step = [&](int j, f32x16_t (&cur)[2], f32x16_t (&nxt)[2]) {
-      if (j + 2 < ntiles) issue_k(j & 1);
-      if (j + 1 < ntiles) {
-        issue_v((j + 1) & 1);
-        qk((j + 1) & 1, nxt);
+    // ---- iteration j (1 <= j < ntiles): O += V(j-1)^T P(j-1) under P(j) = 2^S(j), then S(j+1) ----
+    auto step = [&](int j, const uint32_t (&pprev)[16], uint32_t (&pcur)[16]) {
+      publish();  // K(j+1) and V(j-1) have landed; the buffers of K(j) and V(j-2) are free
+      if (j + 2 < ntiles) issue_k(j & 1);  // K(j+2)
+      const int nv = vit.nvalid();         // valid keys of tile j
+      issue_v(j & 1);                      // V(j)
+      if (nv < BN) mask_tail(s, nv);
+      float ps0, ps1;
+      pv((j - 1) & 1, pprev);
+      exp_pack(s, pcur, ps0, ps1);
+      if (__builtin_amdgcn_ballot_w64(ps0 + ps1 > kOver)) {
+        // raise m to the tile maximum, rescale O and l, redo P(j)
+        const float m_new = fmaxf(m_run, tile_max(s));
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
+        exp_pack(s, pcur, ps0, ps1);
       }
-      bf16x8_t pf[4];
-      softmax(cur, cp.nvalid(), pf);
-      pv(j & 1, pf);
-      cp.next(p);
-      publish();
+      l_run += ps0 + ps1;
+      if (j + 1 < ntiles) qk((j + 1) & 1, s);
     };
-    for (int j = 0; j < ntiles; j += 2) {
-      step(j, s0, s1);
-      if (j + 1 < ntiles) step(j + 1, s1, s0);
+    int j = 1;
+    for (; j + 1 < ntiles; j += 2) {
+      step(j, pa, pb);
+      step(j + 1, pb, pa);
     }
+    if (j < ntiles) step(j, pa, pb);
+    // ---- epilogue: O += V(n-1)^T P(n-1) ----
+    publish();
+    if ((ntiles - 1) & 1)
+      pv(1, pb);
+    else
+      pv(0, pa);
   }
 
   finish_tile<D>(p, wi, b, h, qt, oacc, m_run, pair_sum(l_run));
@@ -851,11 +920,11 @@ inline int64_t grid_blocks(const FlashParams& p) {
   return p.n_full + (nq - p.n_full) * p.split;
 }
 
-template <int D, bool PIPE>
-int launch_flash_direct(const FlashParams& p, hipStream_t st) {
+template <int D>
+int launch_flash_pipe(const FlashParams& p, hipStream_t st) {
   const int64_t nblocks = grid_blocks(p);
   LTX_REQUIRE(nblocks <= 0x7FFFFFFF, "ltx_flash_attn_fwd: grid too large");
-  hipLaunchKernelGGL((flash_fwd_direct_kernel<D, PIPE>), dim3((unsigned)nblocks), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((flash_fwd_pipe_kernel<D>), dim3((unsigned)nblocks), dim3(256), 0, st, p);
   LTX_LAUNCH_CHECK("ltx_flash_attn_fwd");
   return launch_combine<D>(p, st);
 }
@@ -1026,7 +1095,7 @@ extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t 
     int64_t n_full = nq;
     int split = 1;
     if (workspace != nullptr) {
-      const int slots = vkey ? resident_slots(flash_fwd_direct_kernel<128, false>)
+      const int slots = vkey ? resident_slots(flash_fwd_pipe_kernel<128>)
                              : resident_slots(flash_fwd_kernel<128, false, false>);
       plan_split(nq, p.tile_start[n], slots, &n_full, &split);
       if (split > 1 && workspace_bytes_for(nq - n_full, split, D) > workspace_bytes) {
@@ -1044,8 +1113,8 @@ extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t 
     }
   }
   if (vkey) {
-    if (D == 128) return launch_flash_direct<128, false>(p, st);
-    return launch_flash_direct<64, false>(p, st);
+    if (D == 128) return launch_flash_pipe<128>(p, st);
+    return launch_flash_pipe<64>(p, st);
   }
   if (D == 128) {
     if (fp8) return launch_flash<128, true, false>(p, st);

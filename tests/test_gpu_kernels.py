@@ -286,6 +286,43 @@ def test_flash_attn_bf16_vs_fp32(dev, case, vlayout):
     assert (lse.cpu() - torch.logsumexp(s_, -1)).abs().max().item() < 1e-2
 
 
+@pytest.mark.parametrize("vlayout", ["token", "key"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("scales", [(1, 6, 1, 12), (12, 1, 6, 1)], ids=["rising", "falling"])
+def test_flash_attn_logit_range(dev, D, scales, vlayout):
+    """Logit maxima that rise far above (or fall far below) the first tile's:
+    K segments scaled so later tiles exceed the running maximum by tens of
+    base-2 units, which forces the rescale of O, l and m mid-stream."""
+    B, Lq, H = 1, 130, 2
+    lens = [64, 100, 64, 77]
+    g = gen(11)
+    q = randn((B, Lq, H, D), g, torch.bfloat16)
+    ks = [randn((B, n, H, D), g, torch.bfloat16, scale=s) for n, s in zip(lens, scales)]
+    vs = [randn((B, n, H, D), g, torch.bfloat16) for n in lens]
+    cap = -(-(sum(lens) + 64 * len(lens) + 64) // 8) * 8
+    ka = torch.zeros(B, cap, H, D, dtype=torch.bfloat16, device=dev)
+    if vlayout == "token":
+        va = torch.zeros_like(ka)
+    else:
+        va = torch.zeros(B, H, D, cap, dtype=torch.bfloat16, device=dev).permute(0, 3, 1, 2)
+    segs, pos = [], 0
+    for kk, vv in zip(ks, vs):
+        n = kk.shape[1]
+        ka[:, pos:pos + n] = kk.to(dev)
+        va[:, pos:pos + n] = vv.to(dev)
+        segs.append(KVSegment(ka[:, pos:pos + n], va[:, pos:pos + n]))
+        pos = -(-(pos + n + 13) // 8) * 8
+    out = torch.empty(B, Lq, H, D, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(B, H, Lq, dtype=torch.float32, device=dev)
+    kernels.flash_attn(q.to(dev), segs, out, lse=lse)
+    torch.cuda.synchronize()
+    K, V = torch.cat(ks, 1), torch.cat(vs, 1)
+    assert_bf16_close(out, _ref_attn(q, K, V), f"logit range {scales} D{D} {vlayout}")
+    s_ = torch.einsum("bqhd,bkhd->bhqk", q.float(), K.float()) / math.sqrt(D)
+    ref_lse = torch.logsumexp(s_, -1)
+    assert ((lse.cpu() - ref_lse).abs() / ref_lse.abs().clamp_min(1)).max().item() < 1e-3
+
+
 def test_flash_attn_key_mask(dev):
     """Text cross-attention: 1152 queries, 1024 keys, 20% masked with the
     reference's (m-1)*finfo.max additive mask."""

@@ -649,18 +649,6 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
   const int qi = qt * BM + wave * 32 + li;
   const int ntiles = wi.j1 - wi.j0;
 
-  // ---- Q^T fragments, resident for the whole key loop ----
-  bf16x8_t qf[QS];
-  {
-    const bool ok = qi < p.Lq;
-    const uint16_t* qp = p.q + b * p.q_bs + (int64_t)(ok ? qi : 0) * p.q_ls + h * p.q_hs + hg * 8;
-#pragma unroll
-    for (int s = 0; s < QS; ++s) {
-      uint4 v = ok ? *reinterpret_cast<const uint4*>(qp + s * 16) : make_uint4(0, 0, 0, 0);
-      qf[s] = __builtin_bit_cast(bf16x8_t, v);
-    }
-  }
-
   // ---- per-lane load offsets (bytes from a tile's first key), loop invariant ----
   const int row_bytes = (int)(p.kv_ls * 2);
   const int vrow_bytes = (int)(p.v_ds * 2);
@@ -706,53 +694,60 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
     asm volatile("" : "+s"(a));
     return a;
   };
-  auto issue_k = [&](int buf) {
-    const auto rs = __builtin_amdgcn_make_buffer_rsrc((void*)kit.ptr, (short)0, 0x7FFFFFFF, 0x00020000);
-    const int nv = kit.nvalid();
-    const uint32_t l0 = lds_slot0(kbuf[buf]);
-    if (nv == BN) {
-#pragma unroll
-      for (int i = 0; i < KSLOT; ++i)
-        if (wave + 4 * i < KINS) {
-          const int off = koff[i];  // a local: an array element as the offset operand trips clang's host pass
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(uintptr_t)(l0 + i * 4096), 16, off, 0, 0, 0);
-        }
-    } else {
-      // a segment's last, partial tile: rows past its end re-read its last row
-#pragma unroll
-      for (int i = 0; i < KSLOT; ++i)
-        if (wave + 4 * i < KINS) {
-          int r, c;
-          kpos(i, r, c);
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(uintptr_t)(l0 + i * 4096), 16,
-                                                   min(r, nv - 1) * row_bytes + c * 16, 0, 0, 0);
-        }
+  // One load instruction ("slot" i of this wave) of a K or V tile.  rs is the
+  // tile's buffer resource, l0 this wave's first LDS chunk of the buffer and
+  // nv the tile's valid keys (a segment's partial last tile re-reads its last
+  // row / 8-key chunk for the positions past its end).
+  auto k_load = [&](__amdgpu_buffer_rsrc_t rs, uint32_t l0, int nv, int i) {
+    if (i < KSLOT && wave + 4 * i < KINS) {
+      int off = koff[i];
+      if (nv < BN) {
+        int r, c;
+        kpos(i, r, c);
+        off = min(r, nv - 1) * row_bytes + c * 16;
+      }
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(uintptr_t)(l0 + i * 4096), 16, off, 0, 0, 0);
     }
+  };
+  auto v_load = [&](__amdgpu_buffer_rsrc_t rs, uint32_t l0, int nv, int i) {
+    if (i < VSLOT && wave + 4 * i < VINS) {
+      int off = voff[i];
+      if (nv < BN) {
+        int d, c;
+        vpos(i, d, c);
+        off = d * vrow_bytes + min(c, (nv + 7) / 8 - 1) * 16;
+      }
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(uintptr_t)(l0 + i * 4096), 16, off, 0, 0, 0);
+    }
+  };
+  auto rsrc = [&](const char* ptr) { return __builtin_amdgcn_make_buffer_rsrc((void*)ptr, (short)0, 0x7FFFFFFF, 0x00020000); };
+  auto issue_k = [&](int buf) {
+    const auto rs = rsrc(kit.ptr);
+    const uint32_t l0 = lds_slot0(kbuf[buf]);
+    const int nv = kit.nvalid();
+#pragma unroll
+    for (int i = 0; i < KSLOT; ++i) k_load(rs, l0, nv, i);
     kit.next(p.k_ptr, k_head, k_tile, p);
   };
   auto issue_v = [&](int buf) {
-    const auto rs = __builtin_amdgcn_make_buffer_rsrc((void*)vit.ptr, (short)0, 0x7FFFFFFF, 0x00020000);
-    const int nv = vit.nvalid();
+    const auto rs = rsrc(vit.ptr);
     const uint32_t l0 = lds_slot0(vbuf[buf]);
-    if (nv == BN) {
+    const int nv = vit.nvalid();
 #pragma unroll
-      for (int i = 0; i < VSLOT; ++i)
-        if (wave + 4 * i < VINS) {
-          const int off = voff[i];
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(uintptr_t)(l0 + i * 4096), 16, off, 0, 0, 0);
-        }
-    } else {
-      // 8-key chunks past the segment's last one re-read it
-#pragma unroll
-      for (int i = 0; i < VSLOT; ++i)
-        if (wave + 4 * i < VINS) {
-          int d, c;
-          vpos(i, d, c);
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(uintptr_t)(l0 + i * 4096), 16,
-                                                   d * vrow_bytes + min(c, (nv + 7) / 8 - 1) * 16, 0, 0, 0);
-        }
-    }
+    for (int i = 0; i < VSLOT; ++i) v_load(rs, l0, nv, i);
     vit.next(p.v_ptr, v_head, v_tile, p);
+  };
+
+  // ---- Q^T fragments, resident for the whole key loop ----
+  bf16x8_t qf[QS];
+  auto load_q = [&]() {
+    const bool ok = qi < p.Lq;
+    const uint16_t* qp = p.q + b * p.q_bs + (int64_t)(ok ? qi : 0) * p.q_ls + h * p.q_hs + hg * 8;
+#pragma unroll
+    for (int s = 0; s < QS; ++s) {
+      uint4 v = ok ? *reinterpret_cast<const uint4*>(qp + s * 16) : make_uint4(0, 0, 0, 0);
+      qf[s] = __builtin_bit_cast(bf16x8_t, v);
+    }
   };
 
   f32x16_t oacc[DB];
@@ -761,6 +756,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
   const float c = p.scale_log2;
   float m_run = -INFINITY;  // per query, base-2 logit units
   float l_run = 0.0f;       // this lane's share of the row sum
+  const ltx_bf16x2_t ones = __builtin_bit_cast(ltx_bf16x2_t, 0x3F803F80u);  // bf16 pair (1, 1)
 
   // keys past a partial tile's valid count drop out of the softmax (the
   // lane's key is kb*32 + 16*(r/8) + 8*hg + r%8: compare its constant part
@@ -782,59 +778,45 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
       for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][r]);
     return pair_max(mt) * c;
   };
-  const ltx_bf16x2_t ones = __builtin_bit_cast(ltx_bf16x2_t, 0x3F803F80u);  // bf16 pair (1, 1)
   // P = 2^(S*c - m) packed to bf16 pairs (pw[i] holds scores 2i, 2i+1 in
-  // accumulator order), and the per-lane sums of the two key blocks
-  auto exp_pack = [&](const f32x16_t (&s)[2], uint32_t (&pw)[16], float& ps0, float& ps1) {
+  // accumulator order); returns this lane's sum.  Used outside the slot
+  // program (first tile, rescale).
+  auto exp_all = [&](const f32x16_t (&s)[2], uint32_t (&pw)[16]) {
     const float neg_m = -m_run;
-    ps0 = 0.0f;
-    ps1 = 0.0f;
+    float ps = 0.0f;
 #pragma unroll
     for (int i = 0; i < 32; i += 2) {
       const int kb = i >> 4, r = i & 15;
       const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], c, neg_m));
       const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r + 1], c, neg_m));
       pw[i >> 1] = pack_bf16x2(p0, p1);
-      float& ps = kb == 0 ? ps0 : ps1;
       ps = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(ltx_bf16x2_t, pw[i >> 1]), ones, ps, false);
     }
+    return ps;
   };
-  // S = K Q^T from kbuf[buf]
-  auto qk = [&](int buf, f32x16_t (&s)[2]) {
+  // S = K Q^T of a whole tile from kbuf[buf] (first tile only)
+  auto qk_tile = [&](int buf, f32x16_t (&s)[2]) {
     const f32x16_t zero = f32x16_t{};
     const uint16_t* kf = &kbuf[buf][li * KS + hg * 8];
-    bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(kf);
-    bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(kf + 32 * KS);
 #pragma unroll
     for (int k = 0; k < QS; ++k) {
-      bf16x8_t n0 = a0, n1 = a1;
-      if (k + 1 < QS) {
-        n0 = *reinterpret_cast<const bf16x8_t*>(kf + (k + 1) * 16);
-        n1 = *reinterpret_cast<const bf16x8_t*>(kf + 32 * KS + (k + 1) * 16);
-      }
+      const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(kf + k * 16);
+      const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(kf + 32 * KS + k * 16);
       s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[k], k == 0 ? zero : s[0], 0, 0, 0);
       s[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[k], k == 0 ? zero : s[1], 0, 0, 0);
-      a0 = n0;
-      a1 = n1;
     }
   };
-  // O^T += V^T P^T from vbuf[buf]; consecutive MFMAs use different accumulators
-  auto pv = [&](int buf, const uint32_t (&pw)[16]) {
+  // O^T += V^T P^T of a whole tile from vbuf[buf] (last tile only)
+  auto pv_tile = [&](int buf, const uint32_t (&pw)[16]) {
     const uint16_t* vf = &vbuf[buf][li * VS + hg * 8];
-    bf16x8_t va = *reinterpret_cast<const bf16x8_t*>(vf);
 #pragma unroll
     for (int k4 = 0; k4 < 4; ++k4) {
       const bf16x8_t pf =
           __builtin_bit_cast(bf16x8_t, make_uint4(pw[4 * k4], pw[4 * k4 + 1], pw[4 * k4 + 2], pw[4 * k4 + 3]));
 #pragma unroll
-      for (int d = 0; d < DB; ++d) {
-        bf16x8_t na = va;
-        const int nd = d + 1 < DB ? d + 1 : 0;
-        const int nk = d + 1 < DB ? k4 : k4 + 1;
-        if (nk < 4) na = *reinterpret_cast<const bf16x8_t*>(vf + nd * 32 * VS + nk * 16);
-        oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pf, oacc[d], 0, 0, 0);
-        va = na;
-      }
+      for (int d = 0; d < DB; ++d)
+        oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            *reinterpret_cast<const bf16x8_t*>(vf + d * 32 * VS + k4 * 16), pf, oacc[d], 0, 0, 0);
     }
   };
   auto publish = [&]() {
@@ -842,63 +824,128 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
     __syncthreads();
   };
 
+  // ---- the slot program of one tile ----
+  // NS matrix-core slots: PV(j-1) (4*DB MFMAs over vbuf[vb]) then S(j+1)
+  // (2*QS MFMAs over kbuf[kbf]).  Each slot issues its MFMA, the LDS read
+  // of the fragment PREF slots ahead, and a slice of the softmax of S(j):
+  // score pair p (of 16 per lane) has its fma at slot 2p*NS/32, its exp one
+  // step later and its bf16 pack + row-sum dot2 two steps after that.  A
+  // scheduling fence closes every slot, so the exp work stays spread under
+  // the MFMAs (each 32x32x16 MFMA leaves room for about two exp and two
+  // other VALU instructions of the same SIMD).
+  constexpr int NS = 4 * DB + 2 * QS;
+  constexpr int PREF = 3;
+  const uint16_t* vf0 = &vbuf[0][li * VS + hg * 8];
+  const uint16_t* kf0 = &kbuf[0][li * KS + hg * 8];
+  auto tile = [&](int vb, int kbf, const f32x16_t (&scur)[2], f32x16_t (&snext)[2], const uint32_t (&pprev)[16],
+                  uint32_t (&pcur)[16], float& ps0, float& ps1) {
+    const f32x16_t zero = f32x16_t{};
+    const uint16_t* vf = vf0 + vb * VBUF;
+    const uint16_t* kf = kf0 + kbf * KBUF;
+    auto frag = [&](int t) -> bf16x8_t {
+      if (t < 4 * DB) return *reinterpret_cast<const bf16x8_t*>(vf + (t % DB) * 32 * VS + (t / DB) * 16);
+      const int u = t - 4 * DB;
+      return *reinterpret_cast<const bf16x8_t*>(kf + (u / QS) * 32 * KS + (u % QS) * 16);
+    };
+    const float neg_m = -m_run;
+    bf16x8_t ring[PREF + 1];
+#pragma unroll
+    for (int t = 0; t < PREF; ++t) ring[t] = frag(t);
+    float e0[16], e1[16];
+    ps0 = 0.0f;
+    ps1 = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NS + 2; ++t) {
+      if (t < NS) {
+        if (t + PREF < NS) ring[(t + PREF) % (PREF + 1)] = frag(t + PREF);
+        const bf16x8_t a = ring[t % (PREF + 1)];
+        if (t < 4 * DB) {
+          const int k4 = t / DB, d = t % DB;
+          const bf16x8_t pf = __builtin_bit_cast(
+              bf16x8_t, make_uint4(pprev[4 * k4], pprev[4 * k4 + 1], pprev[4 * k4 + 2], pprev[4 * k4 + 3]));
+          oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf, oacc[d], 0, 0, 0);
+        } else {
+          const int u = t - 4 * DB, kb = u / QS, kk = u % QS;
+          snext[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], kk == 0 ? zero : snext[kb], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int kb = q >> 3, r = (q & 7) * 2;
+        if ((2 * q * NS) / 32 == t) {
+          e0[q] = __builtin_fmaf(scur[kb][r], c, neg_m);
+          e1[q] = __builtin_fmaf(scur[kb][r + 1], c, neg_m);
+        }
+        if ((2 * q * NS) / 32 + 1 == t) {
+          e0[q] = __builtin_amdgcn_exp2f(e0[q]);
+          e1[q] = __builtin_amdgcn_exp2f(e1[q]);
+        }
+        if ((2 * q * NS) / 32 + 3 == t || (q == 15 && t == NS + 1 && (2 * q * NS) / 32 + 3 > NS + 1)) {
+          pcur[q] = pack_bf16x2(e0[q], e1[q]);
+          float& ps = (q & 1) ? ps1 : ps0;
+          ps = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(ltx_bf16x2_t, pcur[q]), ones, ps, false);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
   if (ntiles > 0) {
-    f32x16_t s[2];
+    f32x16_t sa[2], sb[2];
     uint32_t pa[16], pb[16];  // P(j) of even / odd j
     // ---- prologue: S(0) sets m from its own maximum; P(0); S(1) ----
     issue_k(0);
     if (ntiles > 1) issue_k(1);
     const int nv0 = vit.nvalid();  // valid keys of tile 0 (the V stream is at tile j before V(j) is issued)
     issue_v(0);
+    load_q();  // its latency overlaps the first tiles' loads
     publish();
-    {
-      qk(0, s);
-      if (nv0 < BN) mask_tail(s, nv0);
-      m_run = tile_max(s);
-      float ps0, ps1;
-      exp_pack(s, pa, ps0, ps1);
-      l_run = ps0 + ps1;
-      if (ntiles > 1) qk(1, s);
-    }
+    qk_tile(0, sa);
+    if (nv0 < BN) mask_tail(sa, nv0);
+    m_run = tile_max(sa);
+    l_run = exp_all(sa, pa);
+    if (ntiles > 1) qk_tile(1, sb);
     if (ntiles > 2) {
       __syncthreads();  // every wave is done with K(0)
       issue_k(0);       // K(2)
     }
-    // ---- iteration j (1 <= j < ntiles): O += V(j-1)^T P(j-1) under P(j) = 2^S(j), then S(j+1) ----
-    auto step = [&](int j, const uint32_t (&pprev)[16], uint32_t (&pcur)[16]) {
+    // ---- iteration j (1 <= j < ntiles): the slot program computes
+    //      O += V(j-1)^T P(j-1), S(j+1) = K(j+1) Q^T and P(j) = 2^(S(j)c - m).
+    //      On the last tile S(j+1) is computed from stale LDS and dropped. ----
+    auto step = [&](int j, f32x16_t (&scur)[2], f32x16_t (&snext)[2], const uint32_t (&pprev)[16],
+                    uint32_t (&pcur)[16]) {
       publish();  // K(j+1) and V(j-1) have landed; the buffers of K(j) and V(j-2) are free
       if (j + 2 < ntiles) issue_k(j & 1);  // K(j+2)
       const int nv = vit.nvalid();         // valid keys of tile j
       issue_v(j & 1);                      // V(j)
-      if (nv < BN) mask_tail(s, nv);
+      if (nv < BN) mask_tail(scur, nv);
       float ps0, ps1;
-      pv((j - 1) & 1, pprev);
-      exp_pack(s, pcur, ps0, ps1);
-      if (__builtin_amdgcn_ballot_w64(ps0 + ps1 > kOver)) {
-        // raise m to the tile maximum, rescale O and l, redo P(j)
-        const float m_new = fmaxf(m_run, tile_max(s));
+      tile((j - 1) & 1, (j + 1) & 1, scur, snext, pprev, pcur, ps0, ps1);
+      float ps = ps0 + ps1;
+      if (__builtin_amdgcn_ballot_w64(ps > kOver)) {
+        // raise m to the tile maximum, rescale O and l, redo P(j) from S(j)
+        const float m_new = fmaxf(m_run, tile_max(scur));
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
         m_run = m_new;
         l_run *= alpha;
 #pragma unroll
         for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
-        exp_pack(s, pcur, ps0, ps1);
+        ps = exp_all(scur, pcur);
       }
-      l_run += ps0 + ps1;
-      if (j + 1 < ntiles) qk((j + 1) & 1, s);
+      l_run += ps;
     };
     int j = 1;
     for (; j + 1 < ntiles; j += 2) {
-      step(j, pa, pb);
-      step(j + 1, pb, pa);
+      step(j, sb, sa, pa, pb);
+      step(j + 1, sa, sb, pb, pa);
     }
-    if (j < ntiles) step(j, pa, pb);
+    if (j < ntiles) step(j, sb, sa, pa, pb);
     // ---- epilogue: O += V(n-1)^T P(n-1) ----
     publish();
     if ((ntiles - 1) & 1)
-      pv(1, pb);
+      pv_tile(1, pb);
     else
-      pv(0, pa);
+      pv_tile(0, pa);
   }
 
   finish_tile<D>(p, wi, b, h, qt, oacc, m_run, pair_sum(l_run));
@@ -961,17 +1008,18 @@ int resident_slots(K kernel) {
 
 
 // Tail q-tiles (those past the last whole round of resident slots) and how
-// many key ranges each is cut into.  Only worth it when there is at least one
-// whole round (otherwise the grid is a single partial round and the extra
-// combine launch costs more than it saves) and each piece keeps >= 4 key
-// tiles.  Zero tail tiles: no split.
+// many key ranges each is cut into: enough pieces to fill the resident slots
+// once more, so the last round drains together with no idle slots.  Only
+// worth it when there is at least one whole round (otherwise the grid is a
+// single partial round and the extra combine launch costs more than it
+// saves) and each piece keeps >= 4 key tiles.  Zero tail tiles: no split.
 inline void plan_split(int64_t nq, int ntiles, int slots, int64_t* n_full, int* split) {
   *n_full = nq;
   *split = 1;
   if (slots <= 0 || nq < slots || nq % slots == 0) return;
   const int64_t full = (nq / slots) * slots;
   const int64_t tail = nq - full;
-  int sp = (int)(slots / (2 * tail));
+  int sp = (int)(slots / tail);
   if (sp > kMaxSplit) sp = kMaxSplit;
   if (sp > ntiles / 4) sp = ntiles / 4;
   if (sp < 2) return;

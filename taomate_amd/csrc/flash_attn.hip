@@ -61,8 +61,8 @@ struct FlashParams {
   // q-tiles is cut into `split` key ranges run by separate workgroups, whose
   // partial results meet in the workspace and are combined by a second kernel.
   int n_full, split;
-  float* part_o;    // [tail tiles * split][kBM][D] unnormalised O
-  float* part_ml;   // [tail tiles * split][kBM][2] running max (log2) and sum
+  uint16_t* part_o;  // [tail tiles * split][kBM][D] bf16 O / l of the key range (0 where l = 0)
+  float* part_ml;     // [tail tiles * split][kBM][2] running max (log2) and sum
   float scale;       // softmax scale applied to q.k
   float scale_log2;  // scale * log2(e)
 };
@@ -236,26 +236,34 @@ __device__ __forceinline__ void finish_tile(const FlashParams& p, const WorkItem
     }
     return;
   }
-  // ---- partial result of one key range: combined by flash_combine_kernel ----
-  float* po = p.part_o + ((int64_t)w.piece * kBM + row) * D;
+  // ---- partial result of one key range: combined by flash_combine_kernel.
+  // O is stored normalised by the range's own sum and rounded to bf16 (the
+  // output's precision), so the partials cost a quarter of fp32 O traffic;
+  // the combine weighs each range by its sum and maximum. ----
+  uint16_t* po = p.part_o + ((int64_t)w.piece * kBM + row) * D;
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
 #pragma unroll
   for (int d = 0; d < DB; ++d)
 #pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4)
-      *reinterpret_cast<float4*>(po + d * 32 + 8 * g4 + 4 * hg) =
-          make_float4(oacc[d][4 * g4], oacc[d][4 * g4 + 1], oacc[d][4 * g4 + 2], oacc[d][4 * g4 + 3]);
+    for (int g4 = 0; g4 < 4; ++g4) {
+      uint2 v;
+      v.x = pack_bf16x2(oacc[d][4 * g4] * inv, oacc[d][4 * g4 + 1] * inv);
+      v.y = pack_bf16x2(oacc[d][4 * g4 + 2] * inv, oacc[d][4 * g4 + 3] * inv);
+      *reinterpret_cast<uint2*>(po + d * 32 + 8 * g4 + 4 * hg) = v;
+    }
   if (hg == 0) *reinterpret_cast<float2*>(p.part_ml + ((int64_t)w.piece * kBM + row) * 2) = make_float2(m_run, l_tot);
 }
 
 constexpr int kMaxSplit = 8;  // key ranges a tail q-tile may be cut into
 
 // Combines the `split` partial results of every tail q-tile, launched after the
-// attention kernel on the same stream.  One thread per (query row, 4 output
-// columns): every piece's (max, sum) and O values are loaded up front, so each
-// thread waits for one round of loads.
+// attention kernel on the same stream: out = sum_i w_i o_i / sum_i w_i with
+// w_i = l_i 2^(m_i - max m) and o_i the range's normalised output.  One thread
+// per (query row, 4 output columns): every piece's (max, sum) and O values
+// are loaded up front, so each thread waits for one round of loads.
 template <int D>
 __global__ void __launch_bounds__(256) flash_combine_kernel(const FlashParams p) {
-  constexpr int C4 = D / 4;             // float4 columns per row
+  constexpr int C4 = D / 4;             // 4-column groups per row
   constexpr int ROWS = 256 / C4;        // rows per workgroup
   constexpr int WG_PER_TILE = kBM / ROWS;
   const int tail = blockIdx.x / WG_PER_TILE;
@@ -269,12 +277,12 @@ __global__ void __launch_bounds__(256) flash_combine_kernel(const FlashParams p)
   if (q >= p.Lq) return;
   const int64_t first = (int64_t)tail * p.split;
   f32x2_t ml[kMaxSplit];
-  float4 o[kMaxSplit];
+  uint2 o[kMaxSplit];
 #pragma unroll
   for (int i = 0; i < kMaxSplit; ++i) {
     if (i < p.split) {
       ml[i] = *reinterpret_cast<const f32x2_t*>(p.part_ml + ((first + i) * kBM + r) * 2);
-      o[i] = *reinterpret_cast<const float4*>(p.part_o + ((first + i) * kBM + r) * D + c4 * 4);
+      o[i] = *reinterpret_cast<const uint2*>(p.part_o + ((first + i) * kBM + r) * D + c4 * 4);
     }
   }
   float mmax = -INFINITY;
@@ -286,9 +294,12 @@ __global__ void __launch_bounds__(256) flash_combine_kernel(const FlashParams p)
 #pragma unroll
   for (int i = 0; i < kMaxSplit; ++i) {
     if (i < p.split) {
-      const float wgt = ml[i][0] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml[i][0] - mmax);
-      lsum += wgt * ml[i][1];
-      acc.x += wgt * o[i].x; acc.y += wgt * o[i].y; acc.z += wgt * o[i].z; acc.w += wgt * o[i].w;
+      const float wgt = ml[i][0] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml[i][0] - mmax) * ml[i][1];
+      lsum += wgt;
+      acc.x += wgt * bf16_bits_to_f32(o[i].x & 0xFFFFu);
+      acc.y += wgt * bf16_bits_to_f32(o[i].x >> 16);
+      acc.z += wgt * bf16_bits_to_f32(o[i].y & 0xFFFFu);
+      acc.w += wgt * bf16_bits_to_f32(o[i].y >> 16);
     }
   }
   const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
@@ -1028,7 +1039,7 @@ inline void plan_split(int64_t nq, int ntiles, int slots, int64_t* n_full, int* 
 }
 
 inline int64_t workspace_bytes_for(int64_t tail, int split, int64_t D) {
-  return tail * split * kBM * (D + 2) * 4;
+  return tail * split * kBM * (2 * 4 + D * 2);  // (max, sum) fp32 + bf16 O row
 }
 
 extern "C" int ltx_flash_attn_workspace_size(int64_t B, int64_t Lq, int64_t H, int64_t D,
@@ -1157,7 +1168,7 @@ extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t 
       LTX_REQUIRE(al(workspace, 256), "ltx_flash_attn_fwd: workspace must be 256-byte aligned");
       const int64_t tail = nq - n_full;
       p.part_ml = static_cast<float*>(workspace);
-      p.part_o = p.part_ml + tail * split * kBM * 2;
+      p.part_o = reinterpret_cast<uint16_t*>(p.part_ml + tail * split * kBM * 2);
     }
   }
   if (vkey) {

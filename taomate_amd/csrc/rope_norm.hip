@@ -92,7 +92,7 @@ __global__ void rope_table_kernel(TOut* __restrict__ cos_out, TOut* __restrict__
 // Fused RMSNorm + SPLIT RoPE.  Block = (H*D)/16 threads; thread (h, c) owns the
 // 8 elements [c*8, c*8+8) of head h's first half and the matching 8 of its
 // second half, i.e. the 8 (x1, x2) rotation pairs j = c*8 .. c*8+7.
-// grid = (rows, B, 2): z selects q (0) or k (1).
+// grid: 1-D, see norm_work (row group, batch element, side q = 0 / k = 1).
 // ---------------------------------------------------------------------------
 struct NormRopeSide {
   const void* in;
@@ -151,13 +151,39 @@ __device__ __forceinline__ float rnd(float v) {
   else return v;
 }
 
+// Rows handled by one workgroup of the fused kernel (all loads of its rows are
+// issued before the first reduction).
+constexpr int NR_ROWS = 1;
+
+// Workgroup -> (row group, batch, side).  The combos (batch, side) of one row
+// group share its RoPE-table rows; blocks are dispatched round-robin over the
+// 8 XCDs (block id % 8), so the combos of a row group are given consecutive
+// blocks of the same XCD and read the table from its L2 after the first.
+struct NormWork {
+  int64_t rg;
+  int b, side;
+};
+__device__ __forceinline__ NormWork norm_work(int ncombo, int B) {
+  const int64_t bid = blockIdx.x;
+  const int64_t x = bid & 7, t = bid >> 3;
+  NormWork w;
+  const int combo = (int)(t % ncombo);
+  w.rg = (t / ncombo) * 8 + x;
+  w.b = combo % B;
+  w.side = combo / B;
+  return w;
+}
+
 template <typename T, typename TT>
 __global__ void __launch_bounds__(256) qk_norm_rope_kernel(NormRopeSide qs, NormRopeSide ks,
-                                                           int H, int D) {
-  const NormRopeSide& sd = (blockIdx.z == 0) ? qs : ks;
-  const int64_t row = blockIdx.x;
-  if (row >= sd.len) return;  // uniform across the block
-  const int b = blockIdx.y;
+                                                           int H, int D, int B, int nsides) {
+  constexpr int R = NR_ROWS;
+  const NormWork wk = norm_work(B * nsides, B);
+  const NormRopeSide& sd = (wk.side == 0) ? qs : ks;
+  const int64_t row0 = wk.rg * R;
+  if (row0 >= sd.len) return;  // uniform across the block
+  const int nr = (int)(sd.len - row0 < R ? sd.len - row0 : R);
+  const int b = wk.b;
   const int HD = H * D;
   const int cpd = D / 16;  // chunks of 8 pairs per head
   const int tid = threadIdx.x;
@@ -166,85 +192,116 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(NormRopeSide qs, Norm
   const int e1 = h * D + c * 8;
   const int e2 = e1 + D / 2;
 
-  const T* in = reinterpret_cast<const T*>(sd.in) + b * sd.in_bs + row * sd.in_ls;
-  Vec8<T> x1, x2;
-  x1.load(in + e1);
-  x2.load(in + e2);
-
-  float v1[8], v2[8];
+  const T* in = reinterpret_cast<const T*>(sd.in) + b * sd.in_bs + row0 * sd.in_ls;
+  Vec8<T> x1[R], x2[R];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    v1[i] = x1.get(i);
-    v2[i] = x2.get(i);
+  for (int r = 0; r < R; ++r)
+    if (r < nr) {
+      x1[r].load(in + r * sd.in_ls + e1);
+      x2[r].load(in + r * sd.in_ls + e2);
+    }
+  const bool rope = sd.cos != nullptr;
+  Vec8<TT> cv[R], sv[R];
+  if (rope) {
+    const TT* cp = reinterpret_cast<const TT*>(sd.cos) + b * sd.tb + h * sd.th + row0 * sd.tt + c * 8;
+    const TT* sp = reinterpret_cast<const TT*>(sd.sin) + b * sd.tb + h * sd.th + row0 * sd.tt + c * 8;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (r < nr) {
+        cv[r].load(cp + r * sd.tt);
+        sv[r].load(sp + r * sd.tt);
+      }
+  }
+  const bool norm = sd.eps >= 0.0f;
+  const bool has_gamma = norm && sd.gamma != nullptr;
+  Vec8<T> g1, g2;
+  if (has_gamma) {
+    g1.load(reinterpret_cast<const T*>(sd.gamma) + e1);
+    g2.load(reinterpret_cast<const T*>(sd.gamma) + e2);
   }
 
-  if (sd.eps >= 0.0f) {
-    float ss = 0.0f;
+  float rs[R];  // 1 / rms of each row
+  if (norm) {
+    float ss[R];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ss += v1[i] * v1[i] + v2[i] * v2[i];
+    for (int r = 0; r < R; ++r) {
+      ss[r] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float a1 = x1[r].get(i), a2 = x2[r].get(i);
+        ss[r] += a1 * a1 + a2 * a2;
+      }
+    }
     // wavefront reduction then across the block's waves through LDS
-    // xor partners stay inside the block (blocks of 16 or 32 threads use part of a wave)
+    // (xor partners stay inside the block: blocks of 16 or 32 threads use part of a wave)
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1)
-      if (off < (int)blockDim.x) ss += __shfl_xor(ss, off, 64);
-    __shared__ float red[16];
+      if (off < (int)blockDim.x)
+#pragma unroll
+        for (int r = 0; r < R; ++r) ss[r] += __shfl_xor(ss[r], off, 64);
+    __shared__ float red[R][4];
     const int wave = tid >> 6, lane = tid & 63;
-    if (lane == 0) red[wave] = ss;
+    if (lane == 0)
+#pragma unroll
+      for (int r = 0; r < R; ++r) red[r][wave] = ss[r];
     __syncthreads();
     const int nwaves = (blockDim.x + 63) >> 6;
-    float tot = 0.0f;
-    for (int w = 0; w < nwaves; ++w) tot += red[w];
-    // y = (x * rsqrt(mean(x^2) + eps)) * gamma in float32, rounded once: the
-    // fused rms_norm of PyTorch (bit-identical to torch.nn.functional.rms_norm
-    // on bf16 rows, checked against it by the tests)
-    const float r = 1.0f / sqrtf(__fadd_rn(__fdiv_rn(tot, (float)HD), sd.eps));
-    Vec8<T> g1, g2;
-    const bool has_gamma = sd.gamma != nullptr;
-    if (has_gamma) {
-      g1.load(reinterpret_cast<const T*>(sd.gamma) + e1);
-      g2.load(reinterpret_cast<const T*>(sd.gamma) + e2);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float tot = 0.0f;
+      for (int w = 0; w < nwaves; ++w) tot += red[r][w];
+      // y = (x * rsqrt(mean(x^2) + eps)) * gamma in float32, rounded once: the
+      // fused rms_norm of PyTorch (bit-identical to torch.nn.functional.rms_norm
+      // on bf16 rows, checked against it by the tests)
+      rs[r] = 1.0f / sqrtf(__fadd_rn(__fdiv_rn(tot, (float)HD), sd.eps));
     }
+  }
+
+  T* out = reinterpret_cast<T*>(sd.out) + b * sd.out_bs + row0 * sd.out_ls;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (r >= nr) break;
+    float v1[8], v2[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      float y1 = __fmul_rn(v1[i], r), y2 = __fmul_rn(v2[i], r);
-      if (has_gamma) {
-        y1 = __fmul_rn(y1, g1.get(i));
-        y2 = __fmul_rn(y2, g2.get(i));
+      v1[i] = x1[r].get(i);
+      v2[i] = x2[r].get(i);
+    }
+    if (norm) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float y1 = __fmul_rn(v1[i], rs[r]), y2 = __fmul_rn(v2[i], rs[r]);
+        if (has_gamma) {
+          y1 = __fmul_rn(y1, g1.get(i));
+          y2 = __fmul_rn(y2, g2.get(i));
+        }
+        v1[i] = rnd<T>(y1);
+        v2[i] = rnd<T>(y2);
       }
-      v1[i] = rnd<T>(y1);
-      v2[i] = rnd<T>(y2);
     }
-  }
-
-  if (sd.cos != nullptr) {
-    const TT* cp = reinterpret_cast<const TT*>(sd.cos) + b * sd.tb + h * sd.th + row * sd.tt + c * 8;
-    const TT* sp = reinterpret_cast<const TT*>(sd.sin) + b * sd.tb + h * sd.th + row * sd.tt + c * 8;
-    Vec8<TT> cv, sv;
-    cv.load(cp);
-    sv.load(sp);
+    if (rope) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float cc = cv[r].get(i), sn = sv[r].get(i);
+        // out1 = x1*c ; out1 += (-s)*x2 ; out2 = x2*c ; out2 += s*x1
+        // (causal_rope.py:121-126: one rounding after the multiply, one after
+        // the float32 multiply-add)
+        const float a1 = rnd<T>(__fmul_rn(v1[i], cc));
+        const float a2 = rnd<T>(__fmul_rn(v2[i], cc));
+        const float o1 = rnd<T>(__fadd_rn(a1, __fmul_rn(-sn, v2[i])));
+        const float o2 = rnd<T>(__fadd_rn(a2, __fmul_rn(sn, v1[i])));
+        v1[i] = o1;
+        v2[i] = o2;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float cc = cv.get(i), s = sv.get(i);
-      // out1 = x1*c ; out1 += (-s)*x2 ; out2 = x2*c ; out2 += s*x1
-      // (causal_rope.py:121-126: one rounding after the multiply, one after
-      // the float32 multiply-add)
-      const float a1 = rnd<T>(__fmul_rn(v1[i], cc));
-      const float a2 = rnd<T>(__fmul_rn(v2[i], cc));
-      const float o1 = rnd<T>(__fadd_rn(a1, __fmul_rn(-s, v2[i])));
-      const float o2 = rnd<T>(__fadd_rn(a2, __fmul_rn(s, v1[i])));
-      v1[i] = o1;
-      v2[i] = o2;
+      x1[r].set(i, v1[i]);
+      x2[r].set(i, v2[i]);
     }
+    x1[r].store(out + r * sd.out_ls + e1);
+    x2[r].store(out + r * sd.out_ls + e2);
   }
-
-  T* out = reinterpret_cast<T*>(sd.out) + b * sd.out_bs + row * sd.out_ls;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    x1.set(i, v1[i]);
-    x2.set(i, v2[i]);
-  }
-  x1.store(out + e1);
-  x2.store(out + e2);
 }
 
 }  // namespace ltx
@@ -344,22 +401,26 @@ extern "C" int ltx_qk_rmsnorm_rope(int dtype, int64_t B, int64_t H, int64_t D,
   const int64_t rows = k_in ? (q_len > k_len ? q_len : k_len) : q_len;
   if (rows == 0) return LTX_OK;
   LTX_REQUIRE(rows <= 0x7FFFFFFF, "ltx_qk_rmsnorm_rope: too many rows");
-  const dim3 grid((unsigned)rows, (unsigned)B, k_in ? 2u : 1u);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int nsides = k_in ? 2 : 1;
+  const int64_t groups = ceil_div(rows, NR_ROWS);
+  const int64_t nblocks = ceil_div(groups, 8) * 8 * B * nsides;
+  LTX_REQUIRE(nblocks <= 0x7FFFFFFF, "ltx_qk_rmsnorm_rope: grid too large");
+  const dim3 grid((unsigned)nblocks);
   if (dtype == LTX_BF16) {
     if (tab_dtype == LTX_BF16)
       hipLaunchKernelGGL((qk_norm_rope_kernel<uint16_t, uint16_t>), grid, dim3((unsigned)threads), 0,
-                         st, qs, ks, (int)H, (int)D);
+                         st, qs, ks, (int)H, (int)D, (int)B, nsides);
     else
       hipLaunchKernelGGL((qk_norm_rope_kernel<uint16_t, float>), grid, dim3((unsigned)threads), 0, st,
-                         qs, ks, (int)H, (int)D);
+                         qs, ks, (int)H, (int)D, (int)B, nsides);
   } else {
     if (tab_dtype == LTX_BF16)
       hipLaunchKernelGGL((qk_norm_rope_kernel<float, uint16_t>), grid, dim3((unsigned)threads), 0, st,
-                         qs, ks, (int)H, (int)D);
+                         qs, ks, (int)H, (int)D, (int)B, nsides);
     else
       hipLaunchKernelGGL((qk_norm_rope_kernel<float, float>), grid, dim3((unsigned)threads), 0, st, qs,
-                         ks, (int)H, (int)D);
+                         ks, (int)H, (int)D, (int)B, nsides);
   }
   LTX_LAUNCH_CHECK("ltx_qk_rmsnorm_rope");
   return LTX_OK;

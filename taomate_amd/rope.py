@@ -122,8 +122,13 @@ def causal_precompute_freqs_cis(
     th = _ntk_theta(theta, dim, grid[0], start_frame, is_audio, rope_extrapolation,
                     rope_train_max_seconds)
     freq = generate_freq_grid(th, nd, dim, dev)
-    out = kernels.rope_table(freq, grid, start_frame, is_audio, [float(m) for m in max_pos[:nd]],
-                             dim, num_attention_heads, batch, dtype)
+    # every batch row has the same grid, so one row of the table is built and
+    # the batch dimension is a stride-0 expansion: the values are the
+    # reference's [B, H, T, dim/(2H)] tables, and the kernels that read them
+    # see one copy (shared through the cache hierarchy) instead of B
+    cos, sin = kernels.rope_table(freq, grid, start_frame, is_audio, [float(m) for m in max_pos[:nd]],
+                                  dim, num_attention_heads, 1, dtype)
+    out = (cos.expand(batch, -1, -1, -1), sin.expand(batch, -1, -1, -1))
     _TABLE_CACHE[key] = out
     while len(_TABLE_CACHE) > _TABLE_CACHE_SIZE:
         _TABLE_CACHE.popitem(last=False)

@@ -100,6 +100,29 @@ def test_qk_rmsnorm_rope_matches_oracle(dev, case):
         assert diff_stats(ko, rk)[0] <= 1e-5
 
 
+@pytest.mark.parametrize("B,L,H,D", [(2, 1152, 32, 128), (1, 192, 8, 64), (2, 37, 16, 64)])
+def test_qk_rmsnorm_rope_shared_table_path(dev, B, L, H, D):
+    """q and k through one RoPE table with a stride-0 batch (the shared-table
+    kernel: one workgroup per positions, all q/k rows) equal, bit for bit, the
+    per-side kernel run on separate per-batch copies of the same table."""
+    g = gen(12)
+    HD = H * D
+    q = randn((B, L, HD), g, torch.bfloat16, 3.0).to(dev)
+    k = randn((B, L, HD), g, torch.bfloat16, 0.5).to(dev)
+    gq = (1 + 0.1 * randn((HD,), g)).to(torch.bfloat16).to(dev)
+    gk = (1 + 0.1 * randn((HD,), g)).to(torch.bfloat16).to(dev)
+    cos, sin = OR.causal_precompute_freqs_cis((1, L, 1), HD, start_frame=5, num_attention_heads=H,
+                                              batch=1, dtype=torch.bfloat16)
+    cs, ss = cos.to(dev).expand(B, -1, -1, -1), sin.to(dev).expand(B, -1, -1, -1)
+    qa, ka = torch.empty_like(q), torch.empty_like(k)
+    kernels.qk_rmsnorm_rope(q, qa, gq, 1e-6, (cs, ss), H, D, k, ka, gk, 1e-6, (cs, ss))
+    qb, kb = torch.empty_like(q), torch.empty_like(k)
+    kernels.qk_rmsnorm_rope(q, qb, gq, 1e-6, (cs.contiguous(), ss.contiguous()), H, D,
+                            k, kb, gk, 1e-6, (cs.contiguous(), ss.contiguous()))
+    torch.cuda.synchronize()
+    assert torch.equal(qa, qb) and torch.equal(ka, kb)
+
+
 def test_norm_only_and_rope_only(dev):
     g = gen(5)
     B, L, H, D = 1, 64, 4, 64

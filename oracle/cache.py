@@ -160,3 +160,80 @@ def streaming_plan(n_blocks: int, video_hw: Tuple[int, int], recent_blocks: int 
                      "video_ids": layer["video_self_k"].flatten().tolist(),
                      "audio_ids": layer["audio_self_k"].flatten().tolist()})
     return plan
+
+
+# ---------------------------------------------------------------------------
+# The anchor | memory | window | current stream (the long-stream steady state).
+#
+# Same mechanics as generate_next_window's commit/evict loop (model.py:202-246,
+# segments as _make_interactive_kv_segment builds them, streaming_runtime.py:
+# 354-387, eviction as _prune_clean_kv_to_sink_recent, :612-662), with the
+# pinned set widened from the sink block to {anchor ("prefix"), memory} and the
+# recent set sized by a frame cap: the window keeps the newest generated
+# blocks whose frames fit in ``window_frames``.  The memory segment keeps its
+# positions (frames anchor_frames .. anchor_frames + memory_frames - 1) and is
+# re-prefilled at them every ``refresh_every`` commits (the re-prefill of
+# retained segments at their original global positions, runtime.py:386-470);
+# its content version counts the refreshes.
+# ---------------------------------------------------------------------------
+PINNED_KINDS = ("prefix", "memory")
+
+
+def retain_pinned_recent(segments: List[Dict], recent_blocks: int,
+                         pinned_kinds=PINNED_KINDS) -> List[int]:
+    """Indices kept: every pinned segment plus the newest ``recent_blocks``
+    other segments, in chronological (list) order."""
+    pinned = [i for i, s in enumerate(segments) if s.get("kind") in pinned_kinds]
+    others = [i for i in range(len(segments)) if i not in pinned]
+    recent = others[-recent_blocks:] if recent_blocks > 0 else []
+    return sorted(set(pinned + recent))
+
+
+def stream_segments_layout(video_hw: Tuple[int, int], anchor_frames: int = 1, memory_frames: int = 2,
+                           chunk_frames: int = 3):
+    """Segment dicts of the anchor and memory, and of generated chunk c."""
+    hw = video_hw[0] * video_hw[1]
+    anchor = {"kind": "prefix", "block_idx": 0, "video_tokens": anchor_frames * hw, "audio_tokens": 0}
+    memory = {"kind": "memory", "block_idx": 1, "video_tokens": memory_frames * hw, "audio_tokens": 0}
+
+    def chunk(c: int) -> Dict:
+        return {"kind": "generated", "block_idx": c + 2, "video_tokens": chunk_frames * hw, "audio_tokens": 0,
+                "window_slot": c}
+    return anchor, memory, chunk
+
+
+def chunk_start_frame(c: int, anchor_frames: int = 1, memory_frames: int = 2, chunk_frames: int = 3) -> int:
+    """Absolute latent frame of chunk c's first frame."""
+    return anchor_frames + memory_frames + c * chunk_frames
+
+
+def streaming_plan_window(n_chunks: int, video_hw: Tuple[int, int], anchor_frames: int = 1,
+                          memory_frames: int = 2, chunk_frames: int = 3, window_frames: int = 12,
+                          refresh_every: int = 4) -> List[dict]:
+    """Replay of the stream on token-id tensors.  Entry c describes the cache
+    after chunk c is committed, evicted and (when due) the memory refreshed:
+    the kept segments, the absolute video token ids in cache order, and the
+    memory content version."""
+    hw = video_hw[0] * video_hw[1]
+    recent = window_frames // chunk_frames
+    anchor, memory, chunk = stream_segments_layout(video_hw, anchor_frames, memory_frames, chunk_frames)
+    ids = lambda f0, nf: torch.arange(f0 * hw, (f0 + nf) * hw, dtype=torch.int64).view(1, -1, 1, 1)
+    layer = {"video_self_k": cat_cache(ids(0, anchor_frames), ids(anchor_frames, memory_frames))}
+    segments = [dict(anchor), dict(memory)]
+    version = 0
+    plan = []
+    for c in range(n_chunks):
+        f0 = chunk_start_frame(c, anchor_frames, memory_frames, chunk_frames)
+        layer["video_self_k"] = cat_cache(layer["video_self_k"], ids(f0, chunk_frames))
+        segments.append(chunk(c))
+        keep = retain_pinned_recent(segments, recent)
+        if keep != list(range(len(segments))):
+            offs = segment_offsets(segments)
+            layer["video_self_k"] = slice_tensor(layer["video_self_k"], [(offs[i][0], offs[i][1]) for i in keep])
+            segments = [dict(segments[i]) for i in keep]
+        if refresh_every > 0 and (c + 1) % refresh_every == 0:
+            # re-prefill the memory at its own positions: same token ids, new version
+            version += 1
+        plan.append({"chunk": c, "segments": [dict(s) for s in segments],
+                     "video_ids": layer["video_self_k"].flatten().tolist(), "memory_version": version})
+    return plan

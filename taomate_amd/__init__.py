@@ -24,6 +24,7 @@ from .cache import (attach_segments, cache_segments, prune_clean_kv_to_sink_rece
 from .kv_cache import (ArenaSpec, KVArena, KVArenaFull, KVCache, KVSpanView, LayerKVCache,
                        _cat_cache, init_kv_cache)
 from .rope import CausalRopeType, apply_split_rotary_emb, causal_precompute_freqs_cis, generate_freq_grid
+from .streaming import ChunkStream, retain_pinned_recent
 
 __all__ = [
     "NativeCallError", "NativeLibraryError", "CausalLTXAttention", "attention_with_cache",
@@ -31,5 +32,5 @@ __all__ = [
     "global_block_at_index", "attach_segments", "cache_segments", "prune_clean_kv_to_sink_recent",
     "retain_streaming_context", "ArenaSpec", "KVArena", "KVArenaFull", "KVCache", "KVSpanView",
     "LayerKVCache", "_cat_cache", "init_kv_cache", "CausalRopeType", "apply_split_rotary_emb",
-    "causal_precompute_freqs_cis", "generate_freq_grid",
+    "causal_precompute_freqs_cis", "generate_freq_grid", "ChunkStream", "retain_pinned_recent",
 ]

@@ -1,0 +1,55 @@
+"""GPU parity of the 60-chunk anchor | memory | window | current stream (one
+attention layer, 8 heads x 64, 3-frame chunks, 12-frame window, 2 memory
+frames re-prefilled every 4 chunks) against the fp32 oracle replay of the same
+policy: every chunk's output, the final cache contents and the segment list.
+bf16 K/V on the 8x12 latent grid; fp8-e4m3 K/V on 8x16 (the fp8 kernel keeps
+one scale per 64-key tile, so a frame must hold a whole number of tiles)."""
+import pytest
+import torch
+
+from oracle import stream as OS
+from taomate_amd.streaming import ChunkStream
+
+from .helpers import BF16_MAX_ABS, FP8_COSINE, assert_bf16_close, cosine, diff_stats
+from .test_gpu_layer import make_layer
+
+pytestmark = pytest.mark.gpu
+
+B, H, DH, N_CHUNKS = 1, 8, 64, 60
+
+
+def _inputs_and_reference(w, grid):
+    """Seeded inputs (bf16-representable, so both sides read the same values)
+    and the oracle's outputs."""
+    g = torch.Generator().manual_seed(51)
+    hw, d = grid[0] * grid[1], H * DH
+    r = lambda nf: torch.randn(B, nf * hw, d, generator=g).to(torch.bfloat16).float()
+    xa, xm = r(1), r(2)
+    chunks = [r(3) for _ in range(N_CHUNKS)]
+    return xa, xm, chunks, OS.run_stream(w, grid, xa, xm, chunks)
+
+
+@pytest.mark.parametrize("kv_dtype,grid", [("bf16", (8, 12)), ("fp8", (8, 16))], ids=["bf16_8x12", "fp8_8x16"])
+def test_chunk_stream_60_chunks(dev, kv_dtype, grid):
+    attn, w = make_layer(dev, H * DH, H, DH, 50)
+    xa, xm, chunks, (ref_outs, ref_k, ref_v, ref_segs) = _inputs_and_reference(w, grid)
+    st = ChunkStream(attn, grid, B, dev, kv_dtype=kv_dtype)
+    worst = 1.0
+    with torch.no_grad():
+        st.prefill(xa.to(dev, torch.bfloat16), xm.to(dev, torch.bfloat16))
+        for c, x in enumerate(chunks):
+            out = st.step(x.to(dev, torch.bfloat16))
+            cs = cosine(out, ref_outs[c])
+            worst = min(worst, cs)
+            if kv_dtype == "bf16":
+                assert_bf16_close(out, ref_outs[c], f"chunk {c}")
+                assert cs >= 0.9999, (c, cs)
+            else:
+                assert cs >= FP8_COSINE, (c, cs)
+                assert diff_stats(out, ref_outs[c])[0] <= BF16_MAX_ABS, c
+    assert st.segments == ref_segs
+    assert st.memory_version == N_CHUNKS // 4
+    bar = 0.9999 if kv_dtype == "bf16" else FP8_COSINE
+    assert cosine(st.k.materialize(), ref_k) >= bar
+    assert cosine(st.v.materialize(), ref_v) >= bar
+    print(f"{kv_dtype}: worst per-chunk cosine {worst:.6f}")

@@ -132,3 +132,41 @@ def test_fp8_reciprocal_fast_path_argument():
     q, qf = x / sc, x * (torch.tensor(1.0) / sc).float()
     assert not torch.equal(q.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8),
                            qf.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8))
+
+
+@pytest.mark.parametrize("window_frames,memory_frames,refresh", [(12, 2, 4), (6, 1, 2), (3, 0, 0), (9, 2, 1)])
+def test_stream_plan_bruteforce(window_frames, memory_frames, refresh):
+    """The anchor | memory | window plan equals its definition written out
+    directly: the anchor frames, the memory frames and the newest
+    window_frames / 3 chunks, in frame order; the memory version counts the
+    refreshes so far."""
+    hw = (2, 3)
+    per = 6
+    for n in range(1, 11):
+        plan = OC.streaming_plan_window(n, hw, anchor_frames=1, memory_frames=memory_frames,
+                                        window_frames=window_frames, refresh_every=refresh)
+        last = plan[-1]
+        keep_chunks = list(range(max(0, n - window_frames // 3), n))
+        frames = [0] + [1 + i for i in range(memory_frames)]
+        for c in keep_chunks:
+            f0 = 1 + memory_frames + 3 * c
+            frames += [f0, f0 + 1, f0 + 2]
+        assert last["video_ids"] == [f * per + t for f in frames for t in range(per)]
+        assert [s["kind"] for s in last["segments"]] == ["prefix", "memory"] + ["generated"] * len(keep_chunks)
+        assert [s.get("window_slot") for s in last["segments"][2:]] == keep_chunks
+        assert last["memory_version"] == (n // refresh if refresh else 0)
+
+
+def test_stream_plan_golden():
+    """Committed fixture of the 16x24 anchor | memory | window stream (60 chunks)."""
+    with open(os.path.join(GOLDEN, "stream_plan_16x24_60.json")) as f:
+        gold = json.load(f)
+    plan = OC.streaming_plan_window(60, (16, 24))
+    assert len(plan) == len(gold) == 60
+    for got, exp in zip(plan, gold):
+        assert got["segments"] == exp["segments"] and got["memory_version"] == exp["memory_version"]
+        v = got["video_ids"]
+        assert v[:3] == exp["video_head"] and v[-3:] == exp["video_tail"] and len(v) == exp["video_len"]
+        assert sum(v) == exp["video_sum"]
+    # steady state: anchor 384 + memory 768 + window 4608 keys before each chunk's own 1152
+    assert gold[-1]["video_len"] == 384 + 768 + 4608

@@ -273,6 +273,8 @@ def main():
     ap.add_argument("--stream-only", action="store_true", help="run only the 60-chunk long-stream measurement")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 256 MiB device copy (scale reference for HBM byte counters)")
+    ap.add_argument("--copy-bandwidth", action="store_true",
+                    help="time plain device copies of 64 MiB - 4 GiB (the practical HBM ceiling of a streaming kernel)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs the hot path on one GPU; --gpus must be 1 "
@@ -290,6 +292,18 @@ def main():
         return
     if args.stream_only:
         print(json.dumps(stream_bench(dev)))
+        return
+    if args.copy_bandwidth:
+        for mib in (64, 256, 1024, 4096):
+            n = mib * 1024 * 1024 // 4
+            x = torch.ones(n, device=dev)
+            y = torch.empty_like(x)
+            for _ in range(10):
+                y.copy_(x)
+            ms = time_region(lambda: y.copy_(x), 50)
+            print(json.dumps({"copy_MiB": mib, "ms": round(ms, 4),
+                              "TB/s (read + write)": round(2 * n * 4 / (ms * 1e-3) / 1e12, 3)}))
+            del x, y
         return
     w = build_workload(dev, args.kv)
     step, attn, norm, append = make_step(w)

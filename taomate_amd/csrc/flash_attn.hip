@@ -122,18 +122,16 @@ struct KVChunk<true> {
     u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
     return make_uint2(v[0], v[1]);
   }
-  // Exact: every e4m3 value is representable in bf16.
+  // Exact: every e4m3 value (subnormals included) is representable in bf16,
+  // and v_cvt_scalef32_pk_bf16_fp8 with scale 1 decodes two codes (bytes 0-1
+  // or 2-3 of the word) into a packed bf16 pair; its output was compared with
+  // the e4m3 definition for every code pair on gfx950.
+  static __device__ __forceinline__ uint32_t pair(uint32_t w, bool hi) {
+    return __builtin_bit_cast(uint32_t, hi ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true)
+                                           : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+  }
   static __device__ __forceinline__ uint4 to_bf16(raw_t r) {
-    uint32_t w[2] = {r.x, r.y};
-    uint32_t o[4];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], false);
-      f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], true);
-      o[2 * i] = (__float_as_uint(lo[0]) >> 16) | (__float_as_uint(lo[1]) & 0xFFFF0000u);
-      o[2 * i + 1] = (__float_as_uint(hi[0]) >> 16) | (__float_as_uint(hi[1]) & 0xFFFF0000u);
-    }
-    return make_uint4(o[0], o[1], o[2], o[3]);
+    return make_uint4(pair(r.x, false), pair(r.x, true), pair(r.y, false), pair(r.y, true));
   }
 };
 
@@ -597,6 +595,17 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 //   while the vector unit turns S(j) into P(j), then S(j+1) = K(j+1) Q^T.
 //   K is loaded two tiles ahead and V one tile ahead of their use; one
 //   barrier per tile frees the buffers read in the previous iteration.
+//
+// fp8 K/V (token-major e4m3 codes with per-(batch, head, frame) scales) use
+// the same slot program.  Their tiles are staged through registers instead:
+// each thread loads 8-byte chunks of the next tiles from HBM one iteration
+// ahead, and after the barrier decodes them (exactly) to bf16 into the free
+// LDS buffers, K rows in the swapped order and V transposed with v_perm, so
+// every code is decoded once per workgroup.  A tile never crosses a frame
+// (frames are whole tiles), so its scales are two scalars: the K scale joins
+// the logit scale, c_j = c * sk_j, and the V scale joins the exponent,
+// P' = 2^(S c_j - m + log2 sv_j) = sv_j P, so the PV MFMAs read plain codes;
+// the row sum and the overflow check use sum(P') / sv_j.
 // ---------------------------------------------------------------------------
 
 // One operand (K or V) of the concatenated segments, walked tile by tile with
@@ -628,9 +637,13 @@ struct KeyStream {
     if (rem <= 0 && s + 1 < p.n_seg) enter(base, head, p, s + 1);
   }
   __device__ __forceinline__ int nvalid() const { return rem < kBN ? rem : kBN; }
+  // first key of the current tile, counted from its segment's start
+  __device__ __forceinline__ int row0(const FlashParams& p) const {
+    return (int)(p.seg_start[s + 1] - p.seg_start[s]) - rem;
+  }
 };
 
-template <int D>
+template <int D, bool FP8>
 __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParams p) {
   constexpr int BM = kBM, BN = kBN;
   constexpr int NKC = D / 8;
@@ -661,7 +674,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
   const int ntiles = wi.j1 - wi.j0;
 
   // ---- per-lane load offsets (bytes from a tile's first key), loop invariant ----
-  const int row_bytes = (int)(p.kv_ls * 2);
+  const int row_bytes = (int)(p.kv_ls * (FP8 ? 1 : 2));
   const int vrow_bytes = (int)(p.v_ds * 2);
   auto kpos = [&](int i, int& r, int& c) {
     const int pch = (wave + 4 * i) * 64 + lane;
@@ -690,10 +703,10 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
     voff[i] = d * vrow_bytes + c * 16;
   }
 
-  const int64_t k_head = (b * p.kv_bs + h * p.kv_hs) * 2;
-  const int64_t v_head = (b * p.v_bs + h * p.v_hs) * 2;
-  const int64_t k_tile = (int64_t)BN * p.kv_ls * 2;
-  constexpr int64_t v_tile = BN * 2;
+  const int64_t k_head = (b * p.kv_bs + h * p.kv_hs) * (FP8 ? 1 : 2);
+  const int64_t v_head = FP8 ? k_head : (b * p.v_bs + h * p.v_hs) * 2;
+  const int64_t k_tile = (int64_t)BN * row_bytes;
+  const int64_t v_tile = FP8 ? k_tile : BN * 2;
   KeyStream kit, vit;
   kit.seek(p.k_ptr, k_head, k_tile, p, wi.j0);
   vit.seek(p.v_ptr, v_head, v_tile, p, wi.j0);
@@ -749,6 +762,73 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
     vit.next(p.v_ptr, v_head, v_tile, p);
   };
 
+  // ---- fp8: register staging of the next K and V tiles ----
+  // K: thread t moves 8-code chunk t % NKC of rows t / NKC + FROWS * i.
+  // V: thread t (< NVP) moves 8-channel chunk t / 16 of keys 4 * (t % 16) .. +3
+  // and writes them transposed (4 keys of 8 channel rows); 16 consecutive
+  // lanes fill one 128-byte V^T row segment, so the LDS writes are
+  // conflict-free.  Loads past a partial tile's last key return 0 (buffer
+  // range check).
+  constexpr int FROWS = 256 / NKC;
+  constexpr int FKL = BN / FROWS;
+  constexpr int NVP = (BN / 4) * NKC;
+  const int tid = threadIdx.x;
+  const int fkc = tid % NKC, fkr = tid / NKC;
+  const int fvg = tid % 16, fvc = tid / 16;
+  const bool fv_on = tid < NVP;
+  uint2 kreg[FP8 ? FKL : 1], vreg[FP8 ? 4 : 1];
+  auto load_k8 = [&]() {
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc((void*)kit.ptr, (short)0, kit.nvalid() * row_bytes, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < FKL; ++i) kreg[i] = KVChunk<true>::bload(rs, (fkr + FROWS * i) * row_bytes + fkc * 8);
+    kit.next(p.k_ptr, k_head, k_tile, p);
+  };
+  auto load_v8 = [&]() {
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc((void*)vit.ptr, (short)0, vit.nvalid() * row_bytes, 0x00020000);
+    if (fv_on) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) vreg[e] = KVChunk<true>::bload(rs, (fvg * 4 + e) * row_bytes + fvc * 8);
+    }
+    vit.next(p.v_ptr, v_head, v_tile, p);
+  };
+  auto store_k8 = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < FKL; ++i)
+      *reinterpret_cast<uint4*>(&kbuf[buf][sig(fkr + FROWS * i) * KS + fkc * 8]) = KVChunk<true>::to_bf16(kreg[i]);
+  };
+  auto store_v8 = [&](int buf) {
+    if (!fv_on) return;
+    uint4 v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = KVChunk<true>::to_bf16(vreg[e]);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t a0 = (&v[0].x)[w], a1 = (&v[1].x)[w], a2 = (&v[2].x)[w], a3 = (&v[3].x)[w];
+      // channels 8*chunk + 2w (low halves) and 2w + 1 (high halves) of keys 4*fvg .. +3
+      uint2 lo, hi;
+      lo.x = __builtin_amdgcn_perm(a1, a0, 0x05040100u);
+      lo.y = __builtin_amdgcn_perm(a3, a2, 0x05040100u);
+      hi.x = __builtin_amdgcn_perm(a1, a0, 0x07060302u);
+      hi.y = __builtin_amdgcn_perm(a3, a2, 0x07060302u);
+      *reinterpret_cast<uint2*>(&vbuf[buf][(fvc * 8 + 2 * w) * VS + fvg * 4]) = lo;
+      *reinterpret_cast<uint2*>(&vbuf[buf][(fvc * 8 + 2 * w + 1) * VS + fvg * 4]) = hi;
+    }
+  };
+  // the tile the softmax works on: its valid keys and (fp8) its scales
+  KeyStream cit;
+  if constexpr (FP8) cit.seek(p.k_ptr, 0, 0, p, wi.j0);
+  struct TileScale { float c, off, inv; };  // logit scale, exponent offset log2 sv, 1 / sv
+  auto tile_scale = [&]() -> TileScale {
+    if constexpr (FP8) {
+      const int64_t o = b * p.sc_bs + h * p.sc_hs + cit.row0(p) / p.frame;
+      const float sk = p.k_sc[cit.s][o];
+      const float sv = p.v_sc[cit.s][o];
+      return TileScale{p.scale_log2 * sk, __log2f(sv), 1.0f / sv};
+    } else {
+      return TileScale{p.scale_log2, 0.0f, 1.0f};
+    }
+  };
+
   // ---- Q^T fragments, resident for the whole key loop ----
   bf16x8_t qf[QS];
   auto load_q = [&]() {
@@ -764,7 +844,6 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
   f32x16_t oacc[DB];
 #pragma unroll
   for (int d = 0; d < DB; ++d) oacc[d] = f32x16_t{};
-  const float c = p.scale_log2;
   float m_run = -INFINITY;  // per query, base-2 logit units
   float l_run = 0.0f;       // this lane's share of the row sum
   const ltx_bf16x2_t ones = __builtin_bit_cast(ltx_bf16x2_t, 0x3F803F80u);  // bf16 pair (1, 1)
@@ -781,7 +860,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
         if (kb * 32 + 16 * (r >> 3) + (r & 7) >= lim) s[kb][r] = -INFINITY;
   };
   // largest base-2 logit of a tile for this lane's query (c > 0)
-  auto tile_max = [&](const f32x16_t (&s)[2]) {
+  auto tile_max = [&](const f32x16_t (&s)[2], float c) {
     float mt = s[0][0];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -789,11 +868,10 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
       for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][r]);
     return pair_max(mt) * c;
   };
-  // P = 2^(S*c - m) packed to bf16 pairs (pw[i] holds scores 2i, 2i+1 in
+  // P = 2^(S*c + off) packed to bf16 pairs (pw[i] holds scores 2i, 2i+1 in
   // accumulator order); returns this lane's sum.  Used outside the slot
   // program (first tile, rescale).
-  auto exp_all = [&](const f32x16_t (&s)[2], uint32_t (&pw)[16]) {
-    const float neg_m = -m_run;
+  auto exp_all = [&](const f32x16_t (&s)[2], uint32_t (&pw)[16], float c, float neg_m) {
     float ps = 0.0f;
 #pragma unroll
     for (int i = 0; i < 32; i += 2) {
@@ -849,7 +927,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
   const uint16_t* vf0 = &vbuf[0][li * VS + hg * 8];
   const uint16_t* kf0 = &kbuf[0][li * KS + hg * 8];
   auto tile = [&](int vb, int kbf, const f32x16_t (&scur)[2], f32x16_t (&snext)[2], const uint32_t (&pprev)[16],
-                  uint32_t (&pcur)[16], float& ps0, float& ps1) {
+                  uint32_t (&pcur)[16], float& ps0, float& ps1, float c, float neg_m) {
     const f32x16_t zero = f32x16_t{};
     const uint16_t* vf = vf0 + vb * VBUF;
     const uint16_t* kf = kf0 + kbf * KBUF;
@@ -858,7 +936,6 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
       const int u = t - 4 * DB;
       return *reinterpret_cast<const bf16x8_t*>(kf + (u / QS) * 32 * KS + (u % QS) * 16);
     };
-    const float neg_m = -m_run;
     bf16x8_t ring[PREF + 1];
 #pragma unroll
     for (int t = 0; t < PREF; ++t) ring[t] = frag(t);
@@ -905,45 +982,87 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
     f32x16_t sa[2], sb[2];
     uint32_t pa[16], pb[16];  // P(j) of even / odd j
     // ---- prologue: S(0) sets m from its own maximum; P(0); S(1) ----
-    issue_k(0);
-    if (ntiles > 1) issue_k(1);
-    const int nv0 = vit.nvalid();  // valid keys of tile 0 (the V stream is at tile j before V(j) is issued)
-    issue_v(0);
-    load_q();  // its latency overlaps the first tiles' loads
-    publish();
+    int nv0;
+    if constexpr (FP8) {
+      // K(0), V(0), K(1) decoded into LDS; K(2) and V(1) left in registers
+      nv0 = cit.nvalid();
+      load_k8();
+      load_v8();
+      load_q();
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      store_k8(0);
+      store_v8(0);
+      if (ntiles > 1) {
+        load_k8();
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        store_k8(1);
+        load_v8();
+      }
+      if (ntiles > 2) load_k8();
+      publish();
+    } else {
+      issue_k(0);
+      if (ntiles > 1) issue_k(1);
+      nv0 = vit.nvalid();  // valid keys of tile 0 (the V stream is at tile j before V(j) is issued)
+      issue_v(0);
+      load_q();  // its latency overlaps the first tiles' loads
+      publish();
+    }
     qk_tile(0, sa);
     if (nv0 < BN) mask_tail(sa, nv0);
-    m_run = tile_max(sa);
-    l_run = exp_all(sa, pa);
+    {
+      const TileScale ts = tile_scale();
+      m_run = tile_max(sa, ts.c);
+      l_run = exp_all(sa, pa, ts.c, ts.off - m_run) * ts.inv;
+      if constexpr (FP8) cit.next(p.k_ptr, 0, 0, p);
+    }
     if (ntiles > 1) qk_tile(1, sb);
     if (ntiles > 2) {
       __syncthreads();  // every wave is done with K(0)
-      issue_k(0);       // K(2)
+      if constexpr (FP8) {
+        store_k8(0);                   // K(2)
+        if (ntiles > 3) load_k8();     // K(3)
+      } else {
+        issue_k(0);                    // K(2)
+      }
     }
     // ---- iteration j (1 <= j < ntiles): the slot program computes
     //      O += V(j-1)^T P(j-1), S(j+1) = K(j+1) Q^T and P(j) = 2^(S(j)c - m).
     //      On the last tile S(j+1) is computed from stale LDS and dropped. ----
     auto step = [&](int j, f32x16_t (&scur)[2], f32x16_t (&snext)[2], const uint32_t (&pprev)[16],
                     uint32_t (&pcur)[16]) {
-      publish();  // K(j+1) and V(j-1) have landed; the buffers of K(j) and V(j-2) are free
-      if (j + 2 < ntiles) issue_k(j & 1);  // K(j+2)
-      const int nv = vit.nvalid();         // valid keys of tile j
-      issue_v(j & 1);                      // V(j)
+      int nv;
+      if constexpr (FP8) {
+        // registers hold K(j+2) and V(j); LDS holds K(j+1) and V(j-1)
+        publish();                          // the buffers of K(j) and V(j-2) are free
+        if (j + 2 < ntiles) store_k8(j & 1);  // K(j+2)
+        store_v8(j & 1);                    // V(j)
+        if (j + 3 < ntiles) load_k8();      // K(j+3)
+        if (j + 1 < ntiles) load_v8();      // V(j+1)
+        nv = cit.nvalid();
+      } else {
+        publish();  // K(j+1) and V(j-1) have landed; the buffers of K(j) and V(j-2) are free
+        if (j + 2 < ntiles) issue_k(j & 1);  // K(j+2)
+        nv = vit.nvalid();                   // valid keys of tile j
+        issue_v(j & 1);                      // V(j)
+      }
       if (nv < BN) mask_tail(scur, nv);
+      const TileScale ts = tile_scale();
       float ps0, ps1;
-      tile((j - 1) & 1, (j + 1) & 1, scur, snext, pprev, pcur, ps0, ps1);
-      float ps = ps0 + ps1;
+      tile((j - 1) & 1, (j + 1) & 1, scur, snext, pprev, pcur, ps0, ps1, ts.c, ts.off - m_run);
+      float ps = (ps0 + ps1) * ts.inv;
       if (__builtin_amdgcn_ballot_w64(ps > kOver)) {
         // raise m to the tile maximum, rescale O and l, redo P(j) from S(j)
-        const float m_new = fmaxf(m_run, tile_max(scur));
+        const float m_new = fmaxf(m_run, tile_max(scur, ts.c));
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
         m_run = m_new;
         l_run *= alpha;
 #pragma unroll
         for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
-        ps = exp_all(scur, pcur);
+        ps = exp_all(scur, pcur, ts.c, ts.off - m_run) * ts.inv;
       }
       l_run += ps;
+      if constexpr (FP8) cit.next(p.k_ptr, 0, 0, p);
     };
     int j = 1;
     for (; j + 1 < ntiles; j += 2) {
@@ -978,11 +1097,11 @@ inline int64_t grid_blocks(const FlashParams& p) {
   return p.n_full + (nq - p.n_full) * p.split;
 }
 
-template <int D>
+template <int D, bool FP8>
 int launch_flash_pipe(const FlashParams& p, hipStream_t st) {
   const int64_t nblocks = grid_blocks(p);
   LTX_REQUIRE(nblocks <= 0x7FFFFFFF, "ltx_flash_attn_fwd: grid too large");
-  hipLaunchKernelGGL((flash_fwd_pipe_kernel<D>), dim3((unsigned)nblocks), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((flash_fwd_pipe_kernel<D, FP8>), dim3((unsigned)nblocks), dim3(256), 0, st, p);
   LTX_LAUNCH_CHECK("ltx_flash_attn_fwd");
   return launch_combine<D>(p, st);
 }
@@ -1154,8 +1273,9 @@ extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t 
     int64_t n_full = nq;
     int split = 1;
     if (workspace != nullptr) {
-      const int slots = vkey ? resident_slots(flash_fwd_pipe_kernel<128>)
-                             : resident_slots(flash_fwd_kernel<128, false, false>);
+      const int slots = vkey ? resident_slots(flash_fwd_pipe_kernel<128, false>)
+                        : fp8  ? resident_slots(flash_fwd_pipe_kernel<128, true>)
+                               : resident_slots(flash_fwd_kernel<128, false, false>);
       plan_split(nq, p.tile_start[n], slots, &n_full, &split);
       if (split > 1 && workspace_bytes_for(nq - n_full, split, D) > workspace_bytes) {
         n_full = nq;
@@ -1172,15 +1292,17 @@ extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t 
     }
   }
   if (vkey) {
-    if (D == 128) return launch_flash_pipe<128>(p, st);
-    return launch_flash_pipe<64>(p, st);
+    if (D == 128) return launch_flash_pipe<128, false>(p, st);
+    return launch_flash_pipe<64, false>(p, st);
+  }
+  if (fp8) {
+    if (D == 128) return launch_flash_pipe<128, true>(p, st);
+    return launch_flash_pipe<64, true>(p, st);
   }
   if (D == 128) {
-    if (fp8) return launch_flash<128, true, false>(p, st);
     if (key_mask) return launch_flash<128, false, true>(p, st);
     return launch_flash<128, false, false>(p, st);
   } else {
-    if (fp8) return launch_flash<64, true, false>(p, st);
     if (key_mask) return launch_flash<64, false, true>(p, st);
     return launch_flash<64, false, false>(p, st);
   }

@@ -397,3 +397,48 @@ def test_flash_attn_fp8_kv(dev, case):
     Kd = OF.dequantize_kv(kc.cpu(), ksc.cpu(), frame)
     Vd = OF.dequantize_kv(vc.cpu(), vsc.cpu(), frame)
     assert_bf16_close(out, _ref_attn(q, Kd, Vd), "fp8 vs dequantised")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("scales", [(1, 1, 1, 1), (1, 6, 1, 12), (12, 1, 6, 1)], ids=["flat", "rising", "falling"])
+def test_flash_attn_fp8_ragged_segments(dev, D, scales):
+    """fp8 K/V in frame-aligned spans with gaps, segments ending mid-tile
+    (partial last frames), per-frame scales spread over two orders of
+    magnitude so later tiles raise the running maximum (rescale path).
+    With scaled segments the softmax is so peaked that e4m3 rounding of K
+    alone moves the fp32 answer (the oracle's own dequantised attention is at
+    cosine 0.995 there), so those cases are held to the dequantised cache."""
+    B, Lq, H, frame = 2, 130, 2, 64
+    lens = [64, 100, 37, 192]
+    g = gen(13)
+    q = randn((B, Lq, H, D), g, torch.bfloat16)
+    ks = [randn((B, n, H, D), g, torch.bfloat16, scale=s) for n, s in zip(lens, scales)]
+    vs = [randn((B, n, H, D), g, torch.bfloat16, scale=s) for n, s in zip(lens, scales)]
+    nfr = [-(-n // frame) for n in lens]
+    cap = (sum(nfr) + len(lens)) * frame
+    kc = torch.zeros(B, cap, H, D, dtype=torch.uint8, device=dev)
+    vc = torch.zeros_like(kc)
+    ksc = torch.ones(B, H, cap // frame, dtype=torch.float32, device=dev)
+    vsc = torch.ones_like(ksc)
+    segs, kd, vd, pos = [], [], [], 0
+    for kk, vv, n, nf in zip(ks, vs, lens, nfr):
+        pad = nf * frame - n
+        kq, kq_s = OF.quantize_kv(torch.nn.functional.pad(kk.float(), (0, 0, 0, 0, 0, pad)), frame)
+        vq, vq_s = OF.quantize_kv(torch.nn.functional.pad(vv.float(), (0, 0, 0, 0, 0, pad)), frame)
+        f0 = pos // frame
+        kc[:, pos:pos + n] = kq[:, :n].to(dev)
+        vc[:, pos:pos + n] = vq[:, :n].to(dev)
+        ksc[:, :, f0:f0 + nf] = kq_s.to(dev)
+        vsc[:, :, f0:f0 + nf] = vq_s.to(dev)
+        segs.append(KVSegment(kc[:, pos:pos + n], vc[:, pos:pos + n], ksc[:, :, f0:f0 + nf], vsc[:, :, f0:f0 + nf]))
+        kd.append(OF.dequantize_kv(kq, kq_s, frame)[:, :n])
+        vd.append(OF.dequantize_kv(vq, vq_s, frame)[:, :n])
+        pos += (nf + 1) * frame   # one free frame between spans
+    out = torch.empty(B, Lq, H, D, dtype=torch.bfloat16, device=dev)
+    kernels.flash_attn(q.to(dev), segs, out, frame_tokens=frame)
+    torch.cuda.synchronize()
+    K, V = torch.cat(ks, 1), torch.cat(vs, 1)
+    if max(scales) == 1:
+        assert cosine(out, _ref_attn(q, K, V)) >= FP8_COSINE
+    assert_bf16_close(out, _ref_attn(q, torch.cat(kd, 1), torch.cat(vd, 1)), f"fp8 ragged {scales} D{D}",
+                      max_abs=2e-2 * max(scales), mean_abs=2e-3 * max(scales))

@@ -209,12 +209,10 @@ __device__ __forceinline__ WorkItem work_item(const FlashParams& p, int bid, int
 // d = db*32 + 8*(r/4) + 4*hg + r%4); m_run / l_tot are per query.
 template <int D>
 __device__ __forceinline__ void finish_tile(const FlashParams& p, const WorkItem& w, int b, int h,
-                                            int qt, const f32x16_t (&oacc)[D / 32], float m_run,
+                                            int qt, int row, const f32x16_t (&oacc)[D / 32], float m_run,
                                             float l_tot) {
   constexpr int DB = D / 32;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int li = lane & 31, hg = lane >> 5;
-  const int row = wave * 32 + li;  // row inside the q-tile
+  const int hg = (threadIdx.x & 63) >> 5;  // row: this lane's query inside the q-tile
   const int qi = qt * kBM + row;
   if (w.piece < 0) {
     if (qi < p.Lq) {
@@ -560,7 +558,8 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(const FlashParams p) 
   }
 
   // ---- epilogue: combine the two lane halves' sums, then store or publish ----
-  finish_tile<D>(p, wi, b, h, qt, oacc, m_run, pair_sum(l_run));
+  finish_tile<D>(p, wi, b, h, qt, (int)(threadIdx.x >> 6) * 32 + (int)(threadIdx.x & 31), oacc, m_run,
+                 pair_sum(l_run));
 }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -745,20 +744,32 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
     }
   };
   auto rsrc = [&](const char* ptr) { return __builtin_amdgcn_make_buffer_rsrc((void*)ptr, (short)0, 0x7FFFFFFF, 0x00020000); };
+  // whole tiles (every tile but a segment's last) take one branch and issue
+  // their loads from the precomputed offsets
   auto issue_k = [&](int buf) {
     const auto rs = rsrc(kit.ptr);
     const uint32_t l0 = lds_slot0(kbuf[buf]);
     const int nv = kit.nvalid();
+    if (nv == BN) {
 #pragma unroll
-    for (int i = 0; i < KSLOT; ++i) k_load(rs, l0, nv, i);
+      for (int i = 0; i < KSLOT; ++i) k_load(rs, l0, BN, i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < KSLOT; ++i) k_load(rs, l0, nv, i);
+    }
     kit.next(p.k_ptr, k_head, k_tile, p);
   };
   auto issue_v = [&](int buf) {
     const auto rs = rsrc(vit.ptr);
     const uint32_t l0 = lds_slot0(vbuf[buf]);
     const int nv = vit.nvalid();
+    if (nv == BN) {
 #pragma unroll
-    for (int i = 0; i < VSLOT; ++i) v_load(rs, l0, nv, i);
+      for (int i = 0; i < VSLOT; ++i) v_load(rs, l0, BN, i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VSLOT; ++i) v_load(rs, l0, nv, i);
+    }
     vit.next(p.v_ptr, v_head, v_tile, p);
   };
 
@@ -934,7 +945,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
     auto frag = [&](int t) -> bf16x8_t {
       if (t < 4 * DB) return *reinterpret_cast<const bf16x8_t*>(vf + (t % DB) * 32 * VS + (t / DB) * 16);
       const int u = t - 4 * DB;
-      return *reinterpret_cast<const bf16x8_t*>(kf + (u / QS) * 32 * KS + (u % QS) * 16);
+      return *reinterpret_cast<const bf16x8_t*>(kf + (u & 1) * 32 * KS + (u >> 1) * 16);
     };
     bf16x8_t ring[PREF + 1];
 #pragma unroll
@@ -953,7 +964,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
               bf16x8_t, make_uint4(pprev[4 * k4], pprev[4 * k4 + 1], pprev[4 * k4 + 2], pprev[4 * k4 + 3]));
           oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf, oacc[d], 0, 0, 0);
         } else {
-          const int u = t - 4 * DB, kb = u / QS, kk = u % QS;
+          const int u = t - 4 * DB, kb = u & 1, kk = u >> 1;  // the two key blocks' chains alternate
           snext[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], kk == 0 ? zero : snext[kb], 0, 0, 0);
         }
       }
@@ -1078,7 +1089,8 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
       pv_tile(0, pa);
   }
 
-  finish_tile<D>(p, wi, b, h, qt, oacc, m_run, pair_sum(l_run));
+  finish_tile<D>(p, wi, b, h, qt, (int)(threadIdx.x >> 6) * 32 + (int)(threadIdx.x & 31), oacc, m_run,
+                 pair_sum(l_run));
 }
 
 template <int D>
@@ -1122,14 +1134,14 @@ using namespace ltx;
 // Resident workgroups the device holds for this kernel (CUs x occupancy),
 // cached per device.
 template <typename K>
-int resident_slots(K kernel) {
-  static int cache[64][2];  // [device] -> {valid, slots}
+int resident_slots(K kernel, int threads = 256) {
+  static int cache[64][2];  // [device] -> {valid, slots}, per kernel
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   if (!cache[dev][0]) {
     int cus = 0, occ = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, 256, 0) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, threads, 0) != hipSuccess) return 0;
     cache[dev][1] = cus * (occ > 0 ? occ : 1);
     cache[dev][0] = 1;
   }

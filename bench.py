@@ -138,8 +138,7 @@ def make_step(w):
 
     def append():
         if a.fp8:
-            kernels.kv_append(kbf, kd, ks, FRAME)
-            kernels.kv_append(w["v_lin"].view(B, LQ, H, D), vd, vs, FRAME)
+            kernels.kv_append_fp8_pair(kbf, kd, ks, w["v_lin"].view(B, LQ, H, D), vd, vs, FRAME)
         else:
             kernels.kv_append(w["v_lin"].view(B, LQ, H, D), vd)
 

@@ -123,6 +123,26 @@ int ltx_kv_append(int src_dtype, int dst_dtype, int64_t B, int64_t L, int64_t H,
                   void* stream);
 
 /*
+ * fp8 append of a chunk's K and V in one launch.
+ * Replaces the two _cat_cache appends of one commit (ltx_causal/transformer/
+ * kv_cache.py:394-398, :2642-2656) for an fp8 arena (the reference has no fp8
+ * cache: an extension of this library).  Same quantisation as ltx_kv_append
+ * with dst_dtype LTX_F8E4M3 (bit-identical codes and scales), for bf16
+ * sources:
+ *   k_src / v_src: bf16 [B, L, H, D] with their own strides (D contiguous);
+ *   k_dst / v_dst: uint8 codes sharing the strides (d_bs, d_ls, d_hs);
+ *   k_scales / v_scales: float32 sharing the strides (sc_bs, sc_hs), frame f of
+ *   (b, h) at scales[b*sc_bs + h*sc_hs + f].  L must be a multiple of
+ *   frame_tokens.
+ */
+int ltx_kv_append_fp8_pair(int64_t B, int64_t L, int64_t H, int64_t D, int64_t frame_tokens,
+                           const void* k_src, int64_t k_bs, int64_t k_ls, int64_t k_hs,
+                           void* k_dst, float* k_scales, const void* v_src, int64_t v_bs,
+                           int64_t v_ls, int64_t v_hs, void* v_dst, float* v_scales,
+                           int64_t d_bs, int64_t d_ls, int64_t d_hs, int64_t sc_bs,
+                           int64_t sc_hs, void* stream);
+
+/*
  * Span gather (cache compaction).
  * Replaces _slice_tensor/_slice_cache (taomate/inference/cache.py:28-56) and
  * _slice_kv_tensor (taomate/inference/streaming_runtime.py:431-442) when a

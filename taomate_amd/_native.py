@@ -37,6 +37,8 @@ SIGNATURES = {
                             _int, _ptr],
     "ltx_kv_append": [_int, _int, _i64, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64,
                       _i64, _i64, _ptr, _i64, _i64, _i64, _ptr],
+    "ltx_kv_append_fp8_pair": [_i64, _i64, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _i64,
+                               _i64, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr],
     "ltx_kv_gather": [_i64, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _i64,
                       _ptr, _ptr, _ptr],
     "ltx_flash_attn_fwd": [_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr,

@@ -230,8 +230,8 @@ def attention_with_cache(
         slot = arena.alloc(real)
         kd, vd = arena.slots("k", slot, real), arena.slots("v", slot, real)
         ks, vs = arena.scale_slots("k", slot, real), arena.scale_slots("v", slot, real)
-        kernels.kv_append(k.view(B, real, H, D), kd, ks, arena.frame_tokens)
-        kernels.kv_append(v_lin.view(B, real, H, D), vd, vs, arena.frame_tokens)
+        kernels.kv_append_fp8_pair(k.view(B, real, H, D), kd, ks, v_lin.view(B, real, H, D), vd, vs,
+                                   arena.frame_tokens)
         new_k = KVSpanView(arena, "k", [(slot, real)])
         new_v = KVSpanView(arena, "v", [(slot, real)])
         segs.append(KVSegment(kd, vd, ks, vs))

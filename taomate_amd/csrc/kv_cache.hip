@@ -81,10 +81,9 @@ __global__ void __launch_bounds__(kQuantThreads) kv_quant_kernel(
       v[4] = bb.x; v[5] = bb.y; v[6] = bb.z; v[7] = bb.w;
     }
   };
-  auto store8 = [&](int idx, const float* v, float sc, float r) {
+  auto store8 = [&](int idx, const float (&v)[8], float sc, float r) {
     float q[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) q[i] = quotient_for_e4m3(v[i], sc, r);
+    quotients_for_e4m3(v, sc, r, q);
     const uint32_t lo = pack4_e4m3(q[0], q[1], q[2], q[3]);
     const uint32_t hi = pack4_e4m3(q[4], q[5], q[6], q[7]);
     const int t = idx / cpr, c = idx % cpr;
@@ -135,6 +134,112 @@ __global__ void __launch_bounds__(kQuantThreads) kv_quant_kernel(
     load8(idx, t);
     store8(idx, t, sc, r);
   }
+}
+
+// fp8 quantise of bf16 rows: one 1024-thread workgroup per (frame, h, b,
+// tensor), each thread holding up to kPairRegs raw 16-byte chunks (8 bf16) of
+// its frame between the absmax pass and the quantise pass, so the frame is
+// read from memory once (chunks past kPairRegs * 1024 are read again).  K and
+// V go in one launch (blockIdx.z = b + B * tensor): a 16x24 frame of 32 x 128
+// heads at B = 2 is 384 workgroups, one round at two workgroups per CU.  The
+// arithmetic is that of kv_quant_kernel, so the codes and scales are
+// bit-identical to it.  (Measured: 256-thread workgroups holding 24 chunks
+// each are slower; the per-thread chain of chunks, not occupancy, bounds it.)
+constexpr int kPairThreads = 1024;
+constexpr int kPairRegs = 8;
+
+struct QuantTensor {
+  const uint16_t* src;
+  int64_t s_bs, s_ls, s_hs;
+  uint8_t* dst;
+  float* scales;
+};
+struct QuantPair {
+  QuantTensor t[2];
+  int64_t d_bs, d_ls, d_hs, sc_bs, sc_hs;
+  int B, frame_tokens, D;
+};
+
+template <int CPR>
+__global__ void __launch_bounds__(kPairThreads) kv_quant_pair_kernel(const QuantPair a) {
+  const int f = blockIdx.x, h = blockIdx.y;
+  const int which = blockIdx.z >= (unsigned)a.B ? 1 : 0;
+  const int b = blockIdx.z - which * a.B;
+  const QuantTensor& T = a.t[which];
+  const int cpr = CPR > 0 ? CPR : a.D / 8;
+  const int n = a.frame_tokens * cpr;
+  const int64_t l0 = (int64_t)f * a.frame_tokens;
+  const uint16_t* sbase = T.src + b * T.s_bs + l0 * T.s_ls + h * T.s_hs;
+  uint8_t* dbase = T.dst + b * a.d_bs + l0 * a.d_ls + h * a.d_hs;
+  auto load = [&](int idx) {
+    const int t = idx / cpr, c = idx % cpr;
+    return *reinterpret_cast<const uint4*>(sbase + (int64_t)t * T.s_ls + c * 8);
+  };
+  auto amax8 = [&](uint4 r, float m) {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      m = fmaxf(m, fmaxf(fabsf(bf16_bits_to_f32(w[i] & 0xFFFFu)), fabsf(bf16_bits_to_f32(w[i] >> 16))));
+    return m;
+  };
+  auto store = [&](int idx, uint4 r, float sc, float rc) {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+    float x[8], q[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = bf16_bits_to_f32(w[i] & 0xFFFFu);
+      x[2 * i + 1] = bf16_bits_to_f32(w[i] >> 16);
+    }
+    quotients_for_e4m3(x, sc, rc, q);
+    const int t = idx / cpr, c = idx % cpr;
+    *reinterpret_cast<uint2*>(dbase + (int64_t)t * a.d_ls + c * 8) =
+        make_uint2(pack4_e4m3(q[0], q[1], q[2], q[3]), pack4_e4m3(q[4], q[5], q[6], q[7]));
+  };
+
+  uint4 raw[kPairRegs];
+#pragma unroll
+  for (int i = 0; i < kPairRegs; ++i) {
+    const int idx = threadIdx.x + i * kPairThreads;
+    raw[i] = idx < n ? load(idx) : make_uint4(0, 0, 0, 0);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kPairRegs; ++i) amax = amax8(raw[i], amax);
+  // keep only the raw chunks live across the reduction (the quantise pass
+  // converts them again instead of holding 8 floats per chunk)
+#pragma unroll
+  for (int i = 0; i < kPairRegs; ++i)
+    asm volatile("" : "+v"(raw[i].x), "+v"(raw[i].y), "+v"(raw[i].z), "+v"(raw[i].w));
+  for (int idx = threadIdx.x + kPairRegs * kPairThreads; idx < n; idx += kPairThreads) amax = amax8(load(idx), amax);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  constexpr int kWaves = kPairThreads / 64;
+  __shared__ float red[kWaves];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  float m = red[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) m = fmaxf(m, red[w]);
+  const float sc = m > 0.0f ? __fdiv_rn(m, 448.0f) : 1.0f;
+  if (threadIdx.x == 0) T.scales[b * a.sc_bs + h * a.sc_hs + f] = sc;
+  const float rc = __fdiv_rn(1.0f, sc);
+#pragma unroll
+  for (int i = 0; i < kPairRegs; ++i) {
+    const int idx = threadIdx.x + i * kPairThreads;
+    if (idx < n) store(idx, raw[i], sc, rc);
+  }
+  for (int idx = threadIdx.x + kPairRegs * kPairThreads; idx < n; idx += kPairThreads) store(idx, load(idx), sc, rc);
+}
+
+inline int launch_quant_pair(const QuantPair& a, int ntensors, int64_t L, int64_t H, hipStream_t st) {
+  const dim3 grid((unsigned)(L / a.frame_tokens), (unsigned)H, (unsigned)(a.B * ntensors));
+  if (a.D == 128)
+    hipLaunchKernelGGL(kv_quant_pair_kernel<16>, grid, dim3(kPairThreads), 0, st, a);
+  else if (a.D == 64)
+    hipLaunchKernelGGL(kv_quant_pair_kernel<8>, grid, dim3(kPairThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL(kv_quant_pair_kernel<0>, grid, dim3(kPairThreads), 0, st, a);
+  return LTX_OK;
 }
 
 // Key-major append: a 64-token x D tile of one (b, h) goes through LDS so both
@@ -276,6 +381,15 @@ extern "C" int ltx_kv_append(int src_dtype, int dst_dtype, int64_t B, int64_t L,
     LTX_REQUIRE(frame_tokens >= 1 && L % frame_tokens == 0,
                 "ltx_kv_append: L (%lld) must be a multiple of frame_tokens (%lld)", (long long)L,
                 (long long)frame_tokens);
+    if (src_dtype == LTX_BF16) {
+      QuantPair a{};
+      a.t[0] = QuantTensor{(const uint16_t*)src, s_bs, s_ls, s_hs, (uint8_t*)dst, scales};
+      a.d_bs = d_bs; a.d_ls = d_ls; a.d_hs = d_hs; a.sc_bs = sc_bs; a.sc_hs = sc_hs;
+      a.B = (int)B; a.frame_tokens = (int)frame_tokens; a.D = (int)D;
+      launch_quant_pair(a, 1, L, H, st);
+      LTX_LAUNCH_CHECK("ltx_kv_append");
+      return LTX_OK;
+    }
     const dim3 grid((unsigned)(L / frame_tokens), (unsigned)H, (unsigned)B);
     auto launch = [&](auto tag, auto cpr) {
       using TS = decltype(tag);
@@ -345,5 +459,36 @@ extern "C" int ltx_kv_gather(int64_t elem_bytes, int64_t B, int64_t H, int64_t D
                      (const uint32_t*)src, s_bs / w, s_ls / w, s_hs / w, (uint32_t*)dst, d_bs / w,
                      d_ls / w, d_hs / w, c, (int)H, wpr);
   LTX_LAUNCH_CHECK("ltx_kv_gather");
+  return LTX_OK;
+}
+
+extern "C" int ltx_kv_append_fp8_pair(int64_t B, int64_t L, int64_t H, int64_t D, int64_t frame_tokens,
+                                      const void* k_src, int64_t k_bs, int64_t k_ls, int64_t k_hs,
+                                      void* k_dst, float* k_scales, const void* v_src, int64_t v_bs,
+                                      int64_t v_ls, int64_t v_hs, void* v_dst, float* v_scales,
+                                      int64_t d_bs, int64_t d_ls, int64_t d_hs, int64_t sc_bs,
+                                      int64_t sc_hs, void* stream) {
+  clear_error();
+  LTX_REQUIRE(B >= 1 && B <= 32767 && L >= 0 && H >= 1 && H <= 65535 && D >= 8 && D % 8 == 0,
+              "ltx_kv_append_fp8_pair: bad shape");
+  LTX_REQUIRE(k_src && v_src && k_dst && v_dst && k_scales && v_scales, "ltx_kv_append_fp8_pair: null pointer");
+  LTX_REQUIRE(frame_tokens >= 1 && L % frame_tokens == 0,
+              "ltx_kv_append_fp8_pair: L (%lld) must be a multiple of frame_tokens (%lld)", (long long)L,
+              (long long)frame_tokens);
+  LTX_REQUIRE(L / frame_tokens <= 0x7FFFFFFF, "ltx_kv_append_fp8_pair: too many frames");
+  auto al = [](const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; };
+  LTX_REQUIRE(al(k_src, 16) && al(v_src, 16) && (k_bs * 2) % 16 == 0 && (k_ls * 2) % 16 == 0 &&
+                  (k_hs * 2) % 16 == 0 && (v_bs * 2) % 16 == 0 && (v_ls * 2) % 16 == 0 && (v_hs * 2) % 16 == 0,
+              "ltx_kv_append_fp8_pair: sources must be 16-byte aligned per row");
+  LTX_REQUIRE(al(k_dst, 8) && al(v_dst, 8) && d_bs % 8 == 0 && d_ls % 8 == 0 && d_hs % 8 == 0,
+              "ltx_kv_append_fp8_pair: destinations must be 8-byte aligned per row");
+  if (L == 0) return LTX_OK;
+  QuantPair a{};
+  a.t[0] = QuantTensor{(const uint16_t*)k_src, k_bs, k_ls, k_hs, (uint8_t*)k_dst, k_scales};
+  a.t[1] = QuantTensor{(const uint16_t*)v_src, v_bs, v_ls, v_hs, (uint8_t*)v_dst, v_scales};
+  a.d_bs = d_bs; a.d_ls = d_ls; a.d_hs = d_hs; a.sc_bs = sc_bs; a.sc_hs = sc_hs;
+  a.B = (int)B; a.frame_tokens = (int)frame_tokens; a.D = (int)D;
+  launch_quant_pair(a, 2, L, H, reinterpret_cast<hipStream_t>(stream));
+  LTX_LAUNCH_CHECK("ltx_kv_append_fp8_pair");
   return LTX_OK;
 }

@@ -68,6 +68,26 @@ __device__ __forceinline__ float quotient_for_e4m3(float x, float sc, float r) {
   return q;
 }
 
+// quotient_for_e4m3 for a chunk of N values with one branch per chunk: the
+// products x * r are straight-line code, and only a chunk holding a lane near
+// a midpoint or in the subnormal range redoes its values with the exact
+// division (same results as quotient_for_e4m3 element by element).
+template <int N>
+__device__ __forceinline__ void quotients_for_e4m3(const float (&x)[N], float sc, float r, float (&q)[N]) {
+  bool slow = false;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    q[i] = x[i] * r;
+    const float a = fabsf(q[i]);
+    const uint32_t low = __float_as_uint(a) & 0xFFFFFu;
+    slow |= (a < 0.015625f) | (low - 0x7FFFCu <= 8u);
+  }
+  if (slow) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) q[i] = quotient_for_e4m3(x[i], sc, r);
+  }
+}
+
 // Four float32 values -> four OCP e4m3fn codes (byte i = value i): clamp to
 // +-448, then the gfx950 converter rounds to nearest even.
 __device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d) {

@@ -88,6 +88,90 @@ __global__ void rope_table_kernel(TOut* __restrict__ cos_out, TOut* __restrict__
   }
 }
 
+// Per-axis position -> fraction of max_pos, float32 IEEE ops exactly as in
+// rope_table_kernel (causal_rope.py:264-277).
+__device__ __forceinline__ float video_frac(int axis, int64_t pos, float max_t, float max_h, float max_w) {
+  if (axis == 0) {
+    const float lt = (float)pos;
+    const float ps = fmaxf(__fadd_rn(__fadd_rn(__fmul_rn(lt, 8.0f), 1.0f), -8.0f), 0.0f);
+    const float pe = fmaxf(__fadd_rn(__fadd_rn(__fmul_rn(__fadd_rn(lt, 1.0f), 8.0f), 1.0f), -8.0f), 0.0f);
+    const float sec = __fdiv_rn(__fdiv_rn(__fadd_rn(ps, pe), 2.0f), 24.0f);
+    return __fdiv_rn(sec, max_t);
+  }
+  const float px = __fadd_rn(__fmul_rn((float)pos, 32.0f), 16.0f);
+  return __fdiv_rn(px, axis == 1 ? max_h : max_w);
+}
+
+// ---------------------------------------------------------------------------
+// Video (3-D) RoPE table, factorised.  A pair's angle depends only on its
+// axis, its frequency index and the token's position along that axis, so a
+// latent frame's grid_h x grid_w tokens share few distinct angles: per head,
+// the t-axis pairs need one value each, the h-axis pairs grid_h and the w-axis
+// pairs grid_w.  One workgroup per (frame, head) computes those cos/sin into
+// LDS with the same float32 operations as rope_table_kernel (so every entry
+// is bit-identical to it), then writes the frame's [T_frame, P] block of the
+// head's table.  The frame's rows are split over blockIdx.z in blocks of
+// kRopeRows rows (each block needs all grid_w column values but only its own
+// row values), so a 3-frame 16x24 chunk of 32 heads is 384 workgroups.
+// About 1/15 of the sines and cosines of rope_table_kernel at that grid.
+// ---------------------------------------------------------------------------
+constexpr int kRopeRows = 4;
+
+template <typename TOut>
+__global__ void __launch_bounds__(256) rope_table_video_kernel(
+    TOut* __restrict__ cos_out, TOut* __restrict__ sin_out, const float* __restrict__ freq_idx, int n_freq,
+    int grid_h, int grid_w, int64_t start_frame, float max_t, float max_h, float max_w, int half_dim,
+    int heads, int64_t T, int batch) {
+  extern __shared__ float fac[];  // [1 + kRopeRows + grid_w][P][2]: t, this block's rows, then columns
+  const int f = blockIdx.x, h = blockIdx.y;
+  const int r0 = blockIdx.z * kRopeRows;
+  const int nr = min(kRopeRows, grid_h - r0);
+  const int P = half_dim / heads;
+  const int pad = half_dim - n_freq * 3;
+  const int rows = 1 + kRopeRows + grid_w;
+  // entry (row, j): row 0 = this frame (t axis), 1..kRopeRows = rows r0.., then columns
+  for (int e = threadIdx.x; e < rows * P; e += blockDim.x) {
+    const int row = e / P, j = e % P;
+    const int g = h * P + j;
+    float c = 1.0f, sn = 0.0f;
+    if (g >= pad) {
+      const int q = g - pad, fi = q / 3, axis = q % 3;
+      const int want = row == 0 ? 0 : (row <= kRopeRows ? 1 : 2);
+      if (axis == want && (axis != 1 || row - 1 < nr)) {
+        const int64_t pos = axis == 0 ? start_frame + f : (axis == 1 ? r0 + row - 1 : row - 1 - kRopeRows);
+        const float frac = video_frac(axis, pos, max_t, max_h, max_w);
+        const float ang = __fmul_rn(freq_idx[fi], __fadd_rn(__fmul_rn(frac, 2.0f), -1.0f));
+        c = cosf(ang);
+        sn = sinf(ang);
+      }
+    }
+    fac[2 * e] = c;
+    fac[2 * e + 1] = sn;
+  }
+  __syncthreads();
+  const int64_t t0 = (int64_t)f * grid_h * grid_w + (int64_t)r0 * grid_w;
+  for (int e = threadIdx.x; e < nr * grid_w * P; e += blockDim.x) {
+    const int tl = e / P, j = e % P;
+    const int g = h * P + j;
+    int row = 0;  // pad entries: identity, stored in every row
+    if (g >= pad) {
+      const int axis = (g - pad) % 3;
+      row = axis == 0 ? 0 : (axis == 1 ? 1 + tl / grid_w : 1 + kRopeRows + tl % grid_w);
+    }
+    const float c = fac[2 * (row * P + j)], sn = fac[2 * (row * P + j) + 1];
+    for (int b = 0; b < batch; ++b) {
+      const int64_t o = (((int64_t)b * heads + h) * T + t0 + tl) * P + j;
+      if constexpr (sizeof(TOut) == 2) {
+        cos_out[o] = f32_to_bf16_bits(c);
+        sin_out[o] = f32_to_bf16_bits(sn);
+      } else {
+        cos_out[o] = c;
+        sin_out[o] = sn;
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Fused RMSNorm + SPLIT RoPE.  Block = (H*D)/16 threads; thread (h, c) owns the
 // 8 elements [c*8, c*8+8) of head h's first half and the matching 8 of its
@@ -330,6 +414,22 @@ extern "C" int ltx_rope_table(void* cos_out, void* sin_out, int out_dtype, const
   const int threads = 256;
   const dim3 grid((unsigned)ceil_div(n, threads));
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int64_t fac_bytes = (1 + kRopeRows + grid_w) * (half / num_heads) * 2 * (int64_t)sizeof(float);
+  if (num_pos_dims == 3 && fac_bytes <= 64 * 1024 && grid_f <= 0x7FFFFFFF && num_heads <= 65535 &&
+      grid_h * grid_w <= 0x7FFFFFFF / (half / num_heads)) {
+    const dim3 vgrid((unsigned)grid_f, (unsigned)num_heads, (unsigned)ceil_div(grid_h, kRopeRows));
+    if (out_dtype == LTX_BF16)
+      hipLaunchKernelGGL(rope_table_video_kernel<uint16_t>, vgrid, dim3(threads), (size_t)fac_bytes, st,
+                         (uint16_t*)cos_out, (uint16_t*)sin_out, freq_idx, (int)n_freq, (int)grid_h,
+                         (int)grid_w, start_frame, max_pos_t, max_pos_h, max_pos_w, half, (int)num_heads, T,
+                         (int)batch);
+    else
+      hipLaunchKernelGGL(rope_table_video_kernel<float>, vgrid, dim3(threads), (size_t)fac_bytes, st,
+                         (float*)cos_out, (float*)sin_out, freq_idx, (int)n_freq, (int)grid_h, (int)grid_w,
+                         start_frame, max_pos_t, max_pos_h, max_pos_w, half, (int)num_heads, T, (int)batch);
+    LTX_LAUNCH_CHECK("ltx_rope_table");
+    return LTX_OK;
+  }
   if (out_dtype == LTX_BF16) {
     hipLaunchKernelGGL(rope_table_kernel<uint16_t>, grid, dim3(threads), 0, st,
                        (uint16_t*)cos_out, (uint16_t*)sin_out, freq_idx, (int)n_freq, num_pos_dims,

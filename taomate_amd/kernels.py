@@ -161,6 +161,37 @@ def kv_append(src: torch.Tensor, dst: torch.Tensor, scales: Optional[torch.Tenso
            int(frame_tokens), _stream(src))
 
 
+def kv_append_fp8_pair(k: torch.Tensor, k_dst: torch.Tensor, k_scales: torch.Tensor, v: torch.Tensor,
+                       v_dst: torch.Tensor, v_scales: torch.Tensor, frame_tokens: int) -> None:
+    """ltx_kv_append_fp8_pair: a chunk's bf16 K and V [B, L, H, D] quantised into
+    fp8 arena slots in one launch (codes and scales as ``kv_append``)."""
+    _need_gpu(k, k_dst, k_scales, v, v_dst, v_scales)
+    if k.dim() != 4 or v.shape != k.shape or k_dst.shape != k.shape or v_dst.shape != k.shape:
+        raise ValueError(f"kv_append_fp8_pair: shapes {tuple(k.shape)}, {tuple(v.shape)}, "
+                         f"{tuple(k_dst.shape)}, {tuple(v_dst.shape)}")
+    if k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise TypeError("kv_append_fp8_pair: K and V must be bf16")
+    if _code(k_dst) != N.F8E4M3 or _code(v_dst) != N.F8E4M3:
+        raise TypeError("kv_append_fp8_pair: destinations must be fp8 (uint8 codes)")
+    if k.stride(3) != 1 or v.stride(3) != 1 or k_dst.stride(3) != 1 or v_dst.stride(3) != 1:
+        raise ValueError("kv_append_fp8_pair: head dim must be contiguous")
+    if k_dst.stride() != v_dst.stride():
+        raise ValueError("kv_append_fp8_pair: K and V destinations must share strides")
+    B, L, H, D = k.shape
+    if L % frame_tokens != 0:
+        raise ValueError(f"kv_append_fp8_pair: L={L} is not a whole number of {frame_tokens}-token frames")
+    for sc in (k_scales, v_scales):
+        if sc.dtype != torch.float32 or sc.shape != (B, H, L // frame_tokens) or (L and sc.stride(2) != 1):
+            raise ValueError(f"kv_append_fp8_pair: scales {tuple(sc.shape)} for L={L}, frame={frame_tokens}")
+    if k_scales.stride() != v_scales.stride():
+        raise ValueError("kv_append_fp8_pair: K and V scales must share strides")
+    N.call("ltx_kv_append_fp8_pair", B, L, H, D, int(frame_tokens),
+           k.data_ptr(), k.stride(0), k.stride(1), k.stride(2), k_dst.data_ptr(), k_scales.data_ptr(),
+           v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), v_dst.data_ptr(), v_scales.data_ptr(),
+           k_dst.stride(0), k_dst.stride(1), k_dst.stride(2), k_scales.stride(0), k_scales.stride(1),
+           _stream(k))
+
+
 def kv_gather(src: torch.Tensor, dst: torch.Tensor, spans: Sequence[Tuple[int, int]]) -> None:
     """ltx_kv_gather: dst[:, 0:sum(len)] = cat(src[:, s:s+len] for s, len in spans)."""
     _need_gpu(src, dst)

@@ -63,8 +63,8 @@ def prefill_kv(attn: CausalLTXAttention, x: torch.Tensor, pe, arena: KVArena) ->
     if arena.fp8:
         k = torch.empty_like(k_lin)
         kernels.qk_rmsnorm_rope(k_lin, k, gk, ek, pe, H, D)
-        kernels.kv_append(k.view(B, L, H, D), kd, arena.scale_slots("k", slot, L), arena.frame_tokens)
-        kernels.kv_append(v_lin.view(B, L, H, D), vd, arena.scale_slots("v", slot, L), arena.frame_tokens)
+        kernels.kv_append_fp8_pair(k.view(B, L, H, D), kd, arena.scale_slots("k", slot, L), v_lin.view(B, L, H, D),
+                                   vd, arena.scale_slots("v", slot, L), arena.frame_tokens)
     else:
         kernels.qk_rmsnorm_rope(k_lin, kd, gk, ek, pe, H, D)
         kernels.kv_append(v_lin.view(B, L, H, D), vd)

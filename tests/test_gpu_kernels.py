@@ -23,6 +23,8 @@ ROPE_CASES = [
     ((75,), 2048, 32, 600, True, [20]),                     # audio 1-D, 32 x 64
     ((3,), 2048, 32, 12, False, [20]),                      # video-time 1-D (cross-modal)
     ((4, 16, 24), 4096, 32, 0, False, [20, 2048, 2048]),    # frame 0 (causal fix clamp)
+    ((1, 8, 130), 4096, 32, 3, False, [20, 2048, 2048]),    # rows too wide for the per-block LDS tables
+    ((2, 18, 20), 4096, 32, 7, False, [20, 2048, 2048]),    # row count not a multiple of the row block
 ]
 
 
@@ -178,6 +180,41 @@ def test_kv_append_fp8_bit_exact(dev, shape, frame):
     torch.cuda.synchronize()
     assert torch.equal(sc.cpu(), sc_ref)
     assert torch.equal(dst.cpu(), codes_ref)
+
+
+@pytest.mark.parametrize("shape,frame", [((2, 1152, 32, 128), 384), ((1, 128, 8, 64), 64),
+                                          ((1, 1024, 4, 128), 512)])
+def test_kv_append_fp8_pair_bit_exact(dev, shape, frame):
+    """K and V of a chunk quantised in one launch into arena slot views (offset
+    spans of a larger store, V read through a strided projection view): codes
+    and scales equal the oracle quantiser and the single-tensor append."""
+    g = gen(14)
+    B, L, H, D = shape
+    k = randn(shape, g, torch.bfloat16, 2.0)
+    v_rows = randn((B, L, H * D + 64), g, torch.bfloat16, 0.5)           # row stride H*D + 64
+    v = v_rows[..., 32:32 + H * D].unflatten(-1, (H, D))
+    k[0, :frame, 1] = 0
+    kd_store = torch.zeros(B, L + 2 * frame, H, D, dtype=torch.uint8, device=dev)
+    vd_store = torch.zeros_like(kd_store)
+    nf = L // frame
+    ks_store = torch.zeros(B, H, nf + 2, dtype=torch.float32, device=dev)
+    vs_store = torch.zeros_like(ks_store)
+    kd, vd = kd_store[:, frame:frame + L], vd_store[:, frame:frame + L]
+    ks, vs = ks_store[:, :, 1:1 + nf], vs_store[:, :, 1:1 + nf]
+    kernels.kv_append_fp8_pair(k.to(dev), kd, ks, v.to(dev), vd, vs, frame)
+    torch.cuda.synchronize()
+    for got_c, got_s, x in ((kd, ks, k), (vd, vs, v)):
+        codes_ref, sc_ref = OF.quantize_kv(x.float(), frame)
+        assert torch.equal(got_s.cpu(), sc_ref)
+        assert torch.equal(got_c.cpu(), codes_ref)
+    # slots and scales outside the spans are untouched
+    assert torch.count_nonzero(kd_store[:, :frame]) == 0 and torch.count_nonzero(vd_store[:, frame + L:]) == 0
+    assert torch.count_nonzero(ks_store[:, :, 0]) == 0 and torch.count_nonzero(vs_store[:, :, 1 + nf:]) == 0
+    one_c = torch.zeros(B, L, H, D, dtype=torch.uint8, device=dev)
+    one_s = torch.zeros(B, H, nf, dtype=torch.float32, device=dev)
+    kernels.kv_append(v.to(dev), one_c, one_s, frame)
+    torch.cuda.synchronize()
+    assert torch.equal(one_c, vd) and torch.equal(one_s, vs)
 
 
 def _frames_to_src(frames, D=64):

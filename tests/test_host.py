@@ -193,6 +193,13 @@ def test_abi_rejects_bad_arguments_without_a_gpu():
     assert rc == -1 and b"head dim" in lib.ltx_last_error()
     rc = lib.ltx_kv_gather(3, 1, 1, 8, None, 0, 0, 0, None, 0, 0, 0, 0, None, None, None)
     assert rc == -1
+    p16 = ctypes.c_void_p(16)
+    rc = lib.ltx_kv_append_fp8_pair(1, 100, 1, 128, 64, p16, 0, 128, 0, p16, p16, p16, 0, 128, 0, p16, p16,
+                                    0, 128, 0, 0, 0, None)
+    assert rc == -1 and b"multiple of frame_tokens" in lib.ltx_last_error()
+    rc = lib.ltx_kv_append_fp8_pair(1, 128, 1, 128, 64, None, 0, 128, 0, p16, p16, p16, 0, 128, 0, p16, p16,
+                                    0, 128, 0, 0, 0, None)
+    assert rc == -1 and b"null pointer" in lib.ltx_last_error()
     with pytest.raises(_native.NativeCallError, match="n_segments"):
         _native.call("ltx_flash_attn_fwd", ctypes.c_void_p(16), 1, 1, 1, 128, 0, 0, 0, 17, None, None,
                      None, 0, 0, 0, 0, 0, 0, 1, 1, None, None, 0, 0, 0, None, 0, ctypes.c_void_p(16), 0,

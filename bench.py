@@ -201,6 +201,103 @@ def stream_bench(dev, n_chunks: int = 60, kv_dtype: str = "fp8", warm_chunks: in
                         "window | current chunk, whole layer per chunk (projections included)"}
 
 
+def dit_bench(dev, steps: int = 5, warmup: int = 2):
+    """One denoising step of the 48-block dual-stream model (video 32 x 128,
+    d = 4096; audio 32 x 64, d = 2048; 4x GELU FFNs; AdaLN modulation) for one
+    512x768 chunk at B = 2: 1152 video tokens over the 3456 cached keys of the
+    chunk workload above, 75 audio tokens over 600 cached, 1024 text tokens
+    (20 % masked) for both streams, A2V / V2A over the chunk's own tokens.
+    Random bf16 weights (seed 3), sigma ~ U(0, 1).  Timed with HIP events
+    around whole steps; the attention share is the summed duration of every
+    attention call (events around each, same stream) over the step time."""
+    from taomate_amd import dit as Dm
+    from taomate_amd import kernels
+    import taomate_amd as T
+    from taomate_amd.kv_cache import KVSpanView
+    from taomate_amd.rope import causal_precompute_freqs_cis
+
+    cfg = Dm.AVConfig()
+    model = Dm.build_model(cfg, dev, seed=3)
+    n_params = sum(p.numel() for p in model.parameters())
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    r = lambda *sh: torch.randn(*sh, generator=g, device=dev).to(torch.bfloat16)
+    LT, LA, LA_C = 1024, 75, 600
+    vlat, alat = r(B, LQ, cfg.in_channels), r(B, LA, cfg.in_channels)
+    sigma = torch.rand(B, generator=g, device=dev)
+    vctx, actx = r(B, LT, cfg.video_dim), r(B, LT, cfg.audio_dim)
+    mask = torch.zeros(B, 1, 1, LT, dtype=torch.bfloat16, device=dev)
+    mask[..., int(0.8 * LT):] = torch.finfo(torch.bfloat16).min
+    cached = LK - LQ
+    specs = {"video_self": T.ArenaSpec(cached + LQ, H, D), "audio_self": T.ArenaSpec(LA_C + LA + 8, 32, 64)}
+    kvc = T.init_kv_cache(cfg.num_layers, B, specs, dev)
+    caches = []
+    for lay in kvc.layers:
+        va, aa = lay.video_self_k.arena, lay.audio_self_k.arena
+        va.slots("k", 0, cached).copy_(r(B, cached, H, D))
+        va.slots("v", 0, cached).copy_(r(B, cached, H, D))
+        aa.slots("k", 0, LA_C).copy_(r(B, LA_C, 32, 64))
+        aa.slots("v", 0, LA_C).copy_(r(B, LA_C, 32, 64))
+        caches.append(T.LayerKVCache(video_self_k=KVSpanView(va, "k", [(0, cached)]),
+                                     video_self_v=KVSpanView(va, "v", [(0, cached)]),
+                                     audio_self_k=KVSpanView(aa, "k", [(0, LA_C)]),
+                                     audio_self_v=KVSpanView(aa, "v", [(0, LA_C)])))
+    pe = lambda grid, dim, heads, f0, audio=False: causal_precompute_freqs_cis(
+        torch.tensor([list(grid)] * B), dim, start_frame=f0, device=dev, dtype=torch.bfloat16,
+        num_attention_heads=heads, is_audio=audio)
+    vpe = pe((3, GRID_H, GRID_W), cfg.video_dim, H, CUR_FRAME0)
+    ape = pe((LA,), cfg.audio_dim, 32, LA_C, True)
+    vcross = [t.repeat_interleave(FRAME, dim=2).contiguous() for t in pe((3,), 2048, 32, CUR_FRAME0)]
+    across = pe((LA,), 2048, 32, LA_C, True)
+
+    attn_events = []
+    real_flash = kernels.flash_attn
+
+    def timed_flash(*a, **kw):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        real_flash(*a, **kw)
+        e1.record()
+        attn_events.append((e0, e1))
+
+    def step():
+        return model.forward_chunk(vlat, alat, sigma, vctx, actx, mask, mask, vpe, ape, vcross, across, caches)
+
+    with torch.no_grad():
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            vo, ao, _ = step()
+        e1.record()
+        e1.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        finite = bool(torch.isfinite(vo).all() and torch.isfinite(ao).all())
+        # attention share: one more step with events around every attention call
+        kernels.flash_attn = timed_flash
+        try:
+            s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s0.record()
+            step()
+            s1.record()
+            s1.synchronize()
+        finally:
+            kernels.flash_attn = real_flash
+        ms_inst = s0.elapsed_time(s1)
+        ms_attn = sum(a.elapsed_time(b) for a, b in attn_events)
+    res = {"ms_per_step": ms, "chunk_query_tokens_per_s": B * LQ / (ms * 1e-3), "params": n_params,
+           "attention_ms": ms_attn, "attention_share": ms_attn / ms_inst, "attention_calls": len(attn_events),
+           "outputs_finite": finite,
+           "workload": "48 dual-stream blocks (video 32x128 d=4096, audio 32x64 d=2048, 4x GELU FFNs, AdaLN), "
+                       "one denoising step of a 512x768 chunk at B=2: 1152 video queries over 3456 cached + 1152 "
+                       "keys, 75 audio over 600 + 75, 1024 text keys (20% masked), A2V 1152x75, V2A 75x1152"}
+    del model, caches, kvc
+    torch.cuda.empty_cache()
+    return res
+
+
 def time_region(fn, iters: int) -> float:
     """Average ms per call over `iters` back-to-back calls, HIP events on the
     launching stream (profiling aid; the reported figures come from the timed
@@ -270,6 +367,8 @@ def main():
     ap.add_argument("--attn-only", action="store_true", help="loop only the attention kernel (profiling)")
     ap.add_argument("--no-stream", action="store_true", help="skip the 60-chunk long-stream measurement")
     ap.add_argument("--stream-only", action="store_true", help="run only the 60-chunk long-stream measurement")
+    ap.add_argument("--no-dit", action="store_true", help="skip the 48-block denoising-step measurement")
+    ap.add_argument("--dit-only", action="store_true", help="run only the 48-block denoising-step measurement")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 256 MiB device copy (scale reference for HBM byte counters)")
     ap.add_argument("--copy-bandwidth", action="store_true",
@@ -291,6 +390,9 @@ def main():
         return
     if args.stream_only:
         print(json.dumps(stream_bench(dev)))
+        return
+    if args.dit_only:
+        print(json.dumps(dit_bench(dev)))
         return
     if args.copy_bandwidth:
         for mib in (64, 256, 1024, 4096):
@@ -378,6 +480,8 @@ def main():
     }
     if not args.no_stream:
         res["long_stream"] = stream_bench(dev)
+    if not args.no_dit:
+        res["dit_step"] = dit_bench(dev)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(res))

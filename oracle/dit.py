@@ -1,0 +1,147 @@
+"""fp32 restatement of the dual-stream block step (oracle; test
+infrastructure only).
+
+Follows, op for op:
+  timestep embedding, AdaLayerNormSingle   ltx_causal/transformer/compat.py:76-275
+  _prepare_timestep / cross timestep       ltx_causal/transformer/causal_model.py:426-496
+  get_ada_values / get_av_ca_ada_values    ltx_causal/transformer/causal_block.py:434-481
+  block_forward_with_cache (sync branch)   ltx_causal/transformer/kv_cache.py:2145-2656
+  text cross-attention without prompt AdaLN  kv_cache.py:1134-1141
+  _process_output                          causal_model.py:568-599
+with the attention calls of ``oracle.attention`` (attention_with_cache for
+self / cross-modal attention, text_cross_attention for the text keys).
+Weights are plain dicts of float32 CPU tensors keyed by the reference's
+parameter names.
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict, List, Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+from . import attention as OA
+
+
+def rms_norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """causal_block.py:94-101 (no weight)."""
+    return F.rms_norm(x, (x.shape[-1],), None, eps)
+
+
+def timestep_embedding(t: torch.Tensor, dim: int = 256, max_period: int = 10000) -> torch.Tensor:
+    """compat.py:76-106, flip_sin_to_cos=True, downscale_freq_shift=0."""
+    half = dim // 2
+    exponent = -math.log(max_period) * torch.arange(half, dtype=torch.float32) / half
+    emb = t[:, None].float() * torch.exp(exponent)[None, :]
+    return torch.cat([torch.cos(emb), torch.sin(emb)], dim=-1)
+
+
+def adaln_single(p: Dict[str, torch.Tensor], prefix: str, t: torch.Tensor):
+    """compat.py:212-275: (linear(silu(emb)), emb), emb = MLP(sinusoid(t))."""
+    e = timestep_embedding(t)
+    e = F.linear(e, p[prefix + "emb.timestep_embedder.linear_1.weight"],
+                 p[prefix + "emb.timestep_embedder.linear_1.bias"])
+    e = F.linear(F.silu(e), p[prefix + "emb.timestep_embedder.linear_2.weight"],
+                 p[prefix + "emb.timestep_embedder.linear_2.bias"])
+    return F.linear(F.silu(e), p[prefix + "linear.weight"], p[prefix + "linear.bias"]), e
+
+
+def ada_values(table: torch.Tensor, batch: int, ts: torch.Tensor, idx: slice):
+    """causal_block.py:434-452."""
+    n = table.shape[0]
+    return (table[idx][None, None] + ts.reshape(batch, ts.shape[1], n, -1)[:, :, idx, :]).unbind(dim=2)
+
+
+def av_ca_values(table: torch.Tensor, batch: int, ss: torch.Tensor, gate: torch.Tensor):
+    """causal_block.py:454-481."""
+    return (*ada_values(table[:4], batch, ss, slice(None)), *ada_values(table[4:], batch, gate, slice(None)))
+
+
+def attn_weights(p: Dict[str, torch.Tensor], prefix: str, heads: int, dim_head: int) -> OA.AttnWeights:
+    g = lambda n: p[prefix + n]
+    return OA.AttnWeights(g("to_q.weight"), g("to_q.bias"), g("to_k.weight"), g("to_k.bias"), g("to_v.weight"),
+                          g("to_v.bias"), g("to_out.0.weight"), g("to_out.0.bias"), g("q_norm.weight"),
+                          g("k_norm.weight"), heads, dim_head)
+
+
+def feed_forward(p: Dict[str, torch.Tensor], prefix: str, x: torch.Tensor) -> torch.Tensor:
+    """compat.py:46-71: Linear -> tanh-GELU -> Linear."""
+    h = F.gelu(F.linear(x, p[prefix + "net.0.proj.weight"], p[prefix + "net.0.proj.bias"]), approximate="tanh")
+    return F.linear(h, p[prefix + "net.2.weight"], p[prefix + "net.2.bias"])
+
+
+def block_forward(p: Dict[str, torch.Tensor], prefix: str, cfg, vx, ax, v_ts, a_ts, video_pe, audio_pe,
+                  video_cross_pe, audio_cross_pe, video_ctx, audio_ctx, video_mask, audio_mask, v_ss, v_gate,
+                  a_ss, a_gate, cache: Dict[str, Optional[torch.Tensor]]):
+    """kv_cache.py:2145-2656, synchronous branch.  ``cache`` holds dense
+    video_self_k/v, audio_self_k/v, a2v_k/v, v2a_k/v (or None).  Returns (vx, ax)."""
+    eps = cfg.norm_eps
+    B = vx.shape[0]
+    vh, vdh, ah, adh = cfg.video_heads, cfg.video_d_head, cfg.audio_heads, cfg.audio_d_head
+    t = lambda n: p[prefix + n]
+    sh, sc, g = ada_values(t("scale_shift_table"), B, v_ts, slice(0, 3))
+    out, _, _ = OA.attention_with_cache(attn_weights(p, prefix + "attn1.", vh, vdh), rms_norm(vx, eps) * (1 + sc) + sh,
+                                        None, video_pe, None, cache.get("video_self_k"), cache.get("video_self_v"))
+    vx = vx + out * g
+    vx = vx + OA.text_cross_attention(attn_weights(p, prefix + "attn2.", vh, vdh), rms_norm(vx, eps), video_ctx,
+                                      video_mask)
+    sh, sc, g = ada_values(t("audio_scale_shift_table"), B, a_ts, slice(0, 3))
+    out, _, _ = OA.attention_with_cache(attn_weights(p, prefix + "audio_attn1.", ah, adh),
+                                        rms_norm(ax, eps) * (1 + sc) + sh, None, audio_pe, None,
+                                        cache.get("audio_self_k"), cache.get("audio_self_v"))
+    ax = ax + out * g
+    ax = ax + OA.text_cross_attention(attn_weights(p, prefix + "audio_attn2.", ah, adh), rms_norm(ax, eps),
+                                      audio_ctx, audio_mask)
+    vn, an = rms_norm(vx, eps), rms_norm(ax, eps)
+    sc_a_a2v, sh_a_a2v, sc_a_v2a, sh_a_v2a, gate_v2a = av_ca_values(t("scale_shift_table_a2v_ca_audio"), B, a_ss,
+                                                                     a_gate)
+    sc_v_a2v, sh_v_a2v, sc_v_v2a, sh_v_v2a, gate_a2v = av_ca_values(t("scale_shift_table_a2v_ca_video"), B, v_ss,
+                                                                     v_gate)
+    a2v, _, _ = OA.attention_with_cache(attn_weights(p, prefix + "audio_to_video_attn.", ah, adh),
+                                        vn * (1 + sc_v_a2v) + sh_v_a2v, an * (1 + sc_a_a2v) + sh_a_a2v,
+                                        video_cross_pe, audio_cross_pe, cache.get("a2v_k"), cache.get("a2v_v"))
+    vx = vx + a2v * gate_a2v
+    v2a, _, _ = OA.attention_with_cache(attn_weights(p, prefix + "video_to_audio_attn.", ah, adh),
+                                        an * (1 + sc_a_v2a) + sh_a_v2a, vn * (1 + sc_v_v2a) + sh_v_v2a,
+                                        audio_cross_pe, video_cross_pe, cache.get("v2a_k"), cache.get("v2a_v"))
+    ax = ax + v2a * gate_v2a
+    sh, sc, g = ada_values(t("scale_shift_table"), B, v_ts, slice(3, 6))
+    vx = vx + feed_forward(p, prefix + "ff.", rms_norm(vx, eps) * (1 + sc) + sh) * g
+    sh, sc, g = ada_values(t("audio_scale_shift_table"), B, a_ts, slice(3, 6))
+    ax = ax + feed_forward(p, prefix + "audio_ff.", rms_norm(ax, eps) * (1 + sc) + sh) * g
+    return vx, ax
+
+
+def forward_chunk(p: Dict[str, torch.Tensor], cfg, video_latent, audio_latent, sigma, video_ctx, audio_ctx,
+                  video_mask, audio_mask, video_pe, audio_pe, video_cross_pe, audio_cross_pe,
+                  caches: List[Dict[str, Optional[torch.Tensor]]]) -> Tuple[torch.Tensor, torch.Tensor]:
+    """One denoising step: patchify, timestep modulation (causal_model.py:426-496),
+    the block loop, the output heads (causal_model.py:568-599)."""
+    B = video_latent.shape[0]
+    vx = F.linear(video_latent, p["patchify_proj.weight"], p["patchify_proj.bias"])
+    ax = F.linear(audio_latent, p["audio_patchify_proj.weight"], p["audio_patchify_proj.bias"])
+    s = (sigma * cfg.timestep_scale_multiplier).flatten()
+    factor = cfg.av_ca_timestep_scale_multiplier / cfg.timestep_scale_multiplier
+    v_ts, v_emb = adaln_single(p, "adaln_single.", s)
+    a_ts, a_emb = adaln_single(p, "audio_adaln_single.", s)
+    v_ss, _ = adaln_single(p, "av_ca_video_scale_shift_adaln_single.", s)
+    a_ss, _ = adaln_single(p, "av_ca_audio_scale_shift_adaln_single.", s)
+    v_gate, _ = adaln_single(p, "av_ca_a2v_gate_adaln_single.", s * factor)
+    a_gate, _ = adaln_single(p, "av_ca_v2a_gate_adaln_single.", s * factor)
+    view = lambda x: x.view(B, -1, x.shape[-1])
+    v_ts, v_emb, a_ts, a_emb = view(v_ts), view(v_emb), view(a_ts), view(a_emb)
+    v_ss, a_ss, v_gate, a_gate = view(v_ss), view(a_ss), view(v_gate), view(a_gate)
+    for i in range(cfg.num_layers):
+        vx, ax = block_forward(p, f"transformer_blocks.{i}.", cfg, vx, ax, v_ts, a_ts, video_pe, audio_pe,
+                               video_cross_pe, audio_cross_pe, video_ctx, audio_ctx, video_mask, audio_mask,
+                               v_ss, v_gate, a_ss, a_gate, caches[i])
+
+    def head(table, proj, x, emb):
+        v = table[None, None] + emb[:, :, None]
+        shift, scale = v[:, :, 0], v[:, :, 1]
+        return F.linear(F.layer_norm(x, (x.shape[-1],), eps=1e-6) * (1 + scale) + shift, p[proj + ".weight"],
+                        p[proj + ".bias"])
+
+    return (head(p["scale_shift_table"], "proj_out", vx, v_emb),
+            head(p["audio_scale_shift_table"], "audio_proj_out", ax, a_emb))

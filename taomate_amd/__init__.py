@@ -25,6 +25,7 @@ from .kv_cache import (ArenaSpec, KVArena, KVArenaFull, KVCache, KVSpanView, Lay
                        _cat_cache, init_kv_cache)
 from .rope import CausalRopeType, apply_split_rotary_emb, causal_precompute_freqs_cis, generate_freq_grid
 from .streaming import ChunkStream, retain_pinned_recent
+from . import dit
 
 __all__ = [
     "NativeCallError", "NativeLibraryError", "CausalLTXAttention", "attention_with_cache",

@@ -149,24 +149,36 @@ __global__ void __launch_bounds__(256) rope_table_video_kernel(
     fac[2 * e + 1] = sn;
   }
   __syncthreads();
+  // write: one thread per (token, 8 consecutive pairs), 16-byte (bf16) or
+  // 2 x 16-byte (float32) stores per table
   const int64_t t0 = (int64_t)f * grid_h * grid_w + (int64_t)r0 * grid_w;
-  for (int e = threadIdx.x; e < nr * grid_w * P; e += blockDim.x) {
-    const int tl = e / P, j = e % P;
-    const int g = h * P + j;
-    int row = 0;  // pad entries: identity, stored in every row
-    if (g >= pad) {
-      const int axis = (g - pad) % 3;
-      row = axis == 0 ? 0 : (axis == 1 ? 1 + tl / grid_w : 1 + kRopeRows + tl % grid_w);
+  const int P8 = P / 8;
+  for (int e = threadIdx.x; e < nr * grid_w * P8; e += blockDim.x) {
+    const int tl = e / P8, j0 = (e % P8) * 8;
+    float c[8], sn[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int j = j0 + i, g = h * P + j;
+      int row = 0;  // pad entries: identity, stored in every row
+      if (g >= pad) {
+        const int axis = (g - pad) % 3;
+        row = axis == 0 ? 0 : (axis == 1 ? 1 + tl / grid_w : 1 + kRopeRows + tl % grid_w);
+      }
+      c[i] = fac[2 * (row * P + j)];
+      sn[i] = fac[2 * (row * P + j) + 1];
     }
-    const float c = fac[2 * (row * P + j)], sn = fac[2 * (row * P + j) + 1];
     for (int b = 0; b < batch; ++b) {
-      const int64_t o = (((int64_t)b * heads + h) * T + t0 + tl) * P + j;
+      const int64_t o = (((int64_t)b * heads + h) * T + t0 + tl) * P + j0;
       if constexpr (sizeof(TOut) == 2) {
-        cos_out[o] = f32_to_bf16_bits(c);
-        sin_out[o] = f32_to_bf16_bits(sn);
+        *reinterpret_cast<uint4*>(cos_out + o) = make_uint4(pack_bf16x2(c[0], c[1]), pack_bf16x2(c[2], c[3]),
+                                                            pack_bf16x2(c[4], c[5]), pack_bf16x2(c[6], c[7]));
+        *reinterpret_cast<uint4*>(sin_out + o) = make_uint4(pack_bf16x2(sn[0], sn[1]), pack_bf16x2(sn[2], sn[3]),
+                                                            pack_bf16x2(sn[4], sn[5]), pack_bf16x2(sn[6], sn[7]));
       } else {
-        cos_out[o] = c;
-        sin_out[o] = sn;
+        reinterpret_cast<float4*>(cos_out + o)[0] = make_float4(c[0], c[1], c[2], c[3]);
+        reinterpret_cast<float4*>(cos_out + o)[1] = make_float4(c[4], c[5], c[6], c[7]);
+        reinterpret_cast<float4*>(sin_out + o)[0] = make_float4(sn[0], sn[1], sn[2], sn[3]);
+        reinterpret_cast<float4*>(sin_out + o)[1] = make_float4(sn[4], sn[5], sn[6], sn[7]);
       }
     }
   }
@@ -415,7 +427,8 @@ extern "C" int ltx_rope_table(void* cos_out, void* sin_out, int out_dtype, const
   const dim3 grid((unsigned)ceil_div(n, threads));
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int64_t fac_bytes = (1 + kRopeRows + grid_w) * (half / num_heads) * 2 * (int64_t)sizeof(float);
-  if (num_pos_dims == 3 && fac_bytes <= 64 * 1024 && grid_f <= 0x7FFFFFFF && num_heads <= 65535 &&
+  if (num_pos_dims == 3 && (half / num_heads) % 8 == 0 && ((uintptr_t)cos_out % 16) == 0 &&
+      ((uintptr_t)sin_out % 16) == 0 && fac_bytes <= 64 * 1024 && grid_f <= 0x7FFFFFFF && num_heads <= 65535 &&
       grid_h * grid_w <= 0x7FFFFFFF / (half / num_heads)) {
     const dim3 vgrid((unsigned)grid_f, (unsigned)num_heads, (unsigned)ceil_div(grid_h, kRopeRows));
     if (out_dtype == LTX_BF16)

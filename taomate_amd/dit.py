@@ -1,0 +1,317 @@
+"""The dual-stream (video + audio) causal DiT around the attention path: one
+denoising step of a chunk through the block stack, on the gfx950 attention
+kernels.
+
+Host mirror, with the reference's module and parameter names so state dicts
+line up:
+  FeedForward / GELUApprox            ltx_causal/transformer/compat.py:28-71
+  Timesteps / TimestepEmbedding /
+  AdaLayerNormSingle                  compat.py:76-275
+  CausalAVTransformerBlock (params)   ltx_causal/transformer/causal_block.py:196-376
+  get_ada_values / get_av_ca_ada_values  causal_block.py:434-481
+  block_forward_with_cache            ltx_causal/transformer/kv_cache.py:2145-2656
+  _apply_text_cross_attention_for_inference  kv_cache.py:1090-1141
+  _prepare_timestep / _prepare_cross_attention_timestep  causal_model.py:426-496
+  _process_output                     causal_model.py:568-599
+
+Built: the shipped inference configuration (no text-cross AdaLN, no gated
+attention, no learned memory adapters, captions already at the model width as
+in the 22B checkpoints).  The q/k/v/out projections, FFNs and AdaLN are
+PyTorch-ROCm GEMMs and elementwise ops; every attention (video self, text
+cross, audio self, text cross, A2V, V2A) runs through this package's kernels.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import List, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .attention import CausalLTXAttention, attention_with_cache
+from .kv_cache import LayerKVCache, _cat_cache
+
+
+def rms_norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """causal_block.py:94-101: RMSNorm over the last dim without a weight."""
+    return F.rms_norm(x, (x.shape[-1],), weight=None, eps=eps)
+
+
+class GELUApprox(nn.Module):
+    def __init__(self, dim_in: int, dim_out: int):
+        super().__init__()
+        self.proj = nn.Linear(dim_in, dim_out)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return F.gelu(self.proj(x), approximate="tanh")
+
+
+class FeedForward(nn.Module):
+    """compat.py:46-71: Linear -> tanh-GELU -> Linear, inner width mult * dim."""
+
+    def __init__(self, dim: int, dim_out: int, mult: int = 4):
+        super().__init__()
+        inner = int(dim * mult)
+        self.net = nn.Sequential(GELUApprox(dim, inner), nn.Identity(), nn.Linear(inner, dim_out))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.net(x)
+
+
+def timestep_embedding(t: torch.Tensor, dim: int = 256, max_period: int = 10000) -> torch.Tensor:
+    """compat.py:76-106 with flip_sin_to_cos=True, downscale_freq_shift=0: [cos | sin]."""
+    half = dim // 2
+    exponent = -math.log(max_period) * torch.arange(half, dtype=torch.float32, device=t.device) / half
+    emb = t[:, None].float() * torch.exp(exponent)[None, :]
+    return torch.cat([torch.cos(emb), torch.sin(emb)], dim=-1)
+
+
+class TimestepEmbedding(nn.Module):
+    def __init__(self, in_channels: int, dim: int):
+        super().__init__()
+        self.linear_1 = nn.Linear(in_channels, dim)
+        self.act = nn.SiLU()
+        self.linear_2 = nn.Linear(dim, dim)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.linear_2(self.act(self.linear_1(x)))
+
+
+class _CombinedEmbedding(nn.Module):
+    def __init__(self, dim: int):
+        super().__init__()
+        self.timestep_embedder = TimestepEmbedding(256, dim)
+
+    def forward(self, t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+        return self.timestep_embedder(timestep_embedding(t).to(dtype))
+
+
+class AdaLayerNormSingle(nn.Module):
+    """compat.py:212-275: timestep -> (coefficient * dim modulation, dim embedding)."""
+
+    def __init__(self, dim: int, coefficient: int = 6):
+        super().__init__()
+        self.emb = _CombinedEmbedding(dim)
+        self.silu = nn.SiLU()
+        self.linear = nn.Linear(dim, coefficient * dim)
+
+    def forward(self, t: torch.Tensor, dtype: torch.dtype) -> Tuple[torch.Tensor, torch.Tensor]:
+        e = self.emb(t, dtype)
+        return self.linear(self.silu(e)), e
+
+
+@dataclass
+class AVConfig:
+    """causal_model.py:97-190 defaults (22B inference configuration)."""
+    num_layers: int = 48
+    video_dim: int = 4096
+    audio_dim: int = 2048
+    video_heads: int = 32
+    audio_heads: int = 32
+    video_d_head: int = 128
+    audio_d_head: int = 64
+    in_channels: int = 128
+    out_channels: int = 128
+    norm_eps: float = 1e-6
+    timestep_scale_multiplier: float = 1000.0
+    av_ca_timestep_scale_multiplier: float = 1.0
+
+
+class AVBlock(nn.Module):
+    """Parameters of CausalAVTransformerBlock (causal_block.py:211-376), same names."""
+
+    def __init__(self, cfg: AVConfig):
+        super().__init__()
+        vd, ad = cfg.video_dim, cfg.audio_dim
+        self.norm_eps = cfg.norm_eps
+        self.attn1 = CausalLTXAttention(vd, heads=cfg.video_heads, dim_head=cfg.video_d_head, norm_eps=cfg.norm_eps)
+        self.attn2 = CausalLTXAttention(vd, context_dim=vd, heads=cfg.video_heads, dim_head=cfg.video_d_head,
+                                        norm_eps=cfg.norm_eps)
+        self.ff = FeedForward(vd, vd)
+        self.scale_shift_table = nn.Parameter(torch.empty(6, vd))
+        self.audio_attn1 = CausalLTXAttention(ad, heads=cfg.audio_heads, dim_head=cfg.audio_d_head,
+                                              norm_eps=cfg.norm_eps)
+        self.audio_attn2 = CausalLTXAttention(ad, context_dim=ad, heads=cfg.audio_heads, dim_head=cfg.audio_d_head,
+                                              norm_eps=cfg.norm_eps)
+        self.audio_ff = FeedForward(ad, ad)
+        self.audio_scale_shift_table = nn.Parameter(torch.empty(6, ad))
+        self.audio_to_video_attn = CausalLTXAttention(vd, context_dim=ad, heads=cfg.audio_heads,
+                                                      dim_head=cfg.audio_d_head, norm_eps=cfg.norm_eps)
+        self.video_to_audio_attn = CausalLTXAttention(ad, context_dim=vd, heads=cfg.audio_heads,
+                                                      dim_head=cfg.audio_d_head, norm_eps=cfg.norm_eps)
+        self.scale_shift_table_a2v_ca_audio = nn.Parameter(torch.empty(5, ad))
+        self.scale_shift_table_a2v_ca_video = nn.Parameter(torch.empty(5, vd))
+
+    @staticmethod
+    def get_ada_values(table: torch.Tensor, batch: int, timestep: torch.Tensor, idx: slice):
+        """causal_block.py:434-452."""
+        n = table.shape[0]
+        return (table[idx].unsqueeze(0).unsqueeze(0).to(device=timestep.device, dtype=timestep.dtype)
+                + timestep.reshape(batch, timestep.shape[1], n, -1)[:, :, idx, :]).unbind(dim=2)
+
+    def get_av_ca_ada_values(self, table: torch.Tensor, batch: int, ss_t: torch.Tensor, gate_t: torch.Tensor):
+        """causal_block.py:454-481: 4 scale/shift values then the gate."""
+        ss = self.get_ada_values(table[:4, :], batch, ss_t, slice(None, None))
+        gate = self.get_ada_values(table[4:, :], batch, gate_t, slice(None, None))
+        return (*ss, *gate)
+
+
+def block_forward_with_cache(block: AVBlock, vx: torch.Tensor, ax: torch.Tensor, v_ts: torch.Tensor,
+                             a_ts: torch.Tensor, video_pe, audio_pe, video_cross_pe, audio_cross_pe,
+                             video_ctx: torch.Tensor, audio_ctx: torch.Tensor, video_mask: Optional[torch.Tensor],
+                             audio_mask: Optional[torch.Tensor], v_cross_ss: torch.Tensor, v_cross_gate: torch.Tensor,
+                             a_cross_ss: torch.Tensor, a_cross_gate: torch.Tensor, cache: LayerKVCache):
+    """kv_cache.py:2145-2656 (synchronous branch): video self -> video text ->
+    audio self -> audio text -> A2V -> V2A -> video FFN -> audio FFN.
+    Returns (vx, ax, cache with the chunk's K/V appended)."""
+    eps = block.norm_eps
+    B = vx.shape[0]
+    # video self-attention
+    sh, sc, g = block.get_ada_values(block.scale_shift_table, B, v_ts, slice(0, 3))
+    out, vs_k, vs_v = attention_with_cache(block.attn1, rms_norm(vx, eps) * (1 + sc) + sh, None, video_pe, None,
+                                           cache.video_self_k, cache.video_self_v)
+    vx = vx + out * g
+    # video text cross-attention (kv_cache.py:1134-1141, no prompt AdaLN)
+    vx = vx + block.attn2(rms_norm(vx, eps), context=video_ctx, mask=video_mask)
+    # audio self-attention
+    sh, sc, g = block.get_ada_values(block.audio_scale_shift_table, B, a_ts, slice(0, 3))
+    out, as_k, as_v = attention_with_cache(block.audio_attn1, rms_norm(ax, eps) * (1 + sc) + sh, None, audio_pe,
+                                           None, cache.audio_self_k, cache.audio_self_v)
+    ax = ax + out * g
+    ax = ax + block.audio_attn2(rms_norm(ax, eps), context=audio_ctx, mask=audio_mask)
+    # cross-modal: both read the norms taken before either update
+    vn, an = rms_norm(vx, eps), rms_norm(ax, eps)
+    sc_a_a2v, sh_a_a2v, sc_a_v2a, sh_a_v2a, gate_v2a = block.get_av_ca_ada_values(
+        block.scale_shift_table_a2v_ca_audio, B, a_cross_ss, a_cross_gate)
+    sc_v_a2v, sh_v_a2v, sc_v_v2a, sh_v_v2a, gate_a2v = block.get_av_ca_ada_values(
+        block.scale_shift_table_a2v_ca_video, B, v_cross_ss, v_cross_gate)
+    vx_a2v = vn * (1 + sc_v_a2v) + sh_v_a2v
+    ax_a2v = an * (1 + sc_a_a2v) + sh_a_a2v
+    ax_v2a = an * (1 + sc_a_v2a) + sh_a_v2a
+    vx_v2a = vn * (1 + sc_v_v2a) + sh_v_v2a
+    a2v, a2v_k, a2v_v = attention_with_cache(block.audio_to_video_attn, vx_a2v, ax_a2v, video_cross_pe,
+                                             audio_cross_pe, cache.a2v_k, cache.a2v_v)
+    vx = vx + a2v * gate_a2v
+    v2a, v2a_k, v2a_v = attention_with_cache(block.video_to_audio_attn, ax_v2a, vx_v2a, audio_cross_pe,
+                                             video_cross_pe, cache.v2a_k, cache.v2a_v)
+    ax = ax + v2a * gate_v2a
+    # feed-forward
+    sh, sc, g = block.get_ada_values(block.scale_shift_table, B, v_ts, slice(3, 6))
+    vx = vx + block.ff(rms_norm(vx, eps) * (1 + sc) + sh) * g
+    sh, sc, g = block.get_ada_values(block.audio_scale_shift_table, B, a_ts, slice(3, 6))
+    ax = ax + block.audio_ff(rms_norm(ax, eps) * (1 + sc) + sh) * g
+    new_cache = LayerKVCache(
+        video_self_k=_cat_cache(cache.video_self_k, vs_k), video_self_v=_cat_cache(cache.video_self_v, vs_v),
+        audio_self_k=_cat_cache(cache.audio_self_k, as_k), audio_self_v=_cat_cache(cache.audio_self_v, as_v),
+        a2v_k=_cat_cache(cache.a2v_k, a2v_k), a2v_v=_cat_cache(cache.a2v_v, a2v_v),
+        v2a_k=_cat_cache(cache.v2a_k, v2a_k), v2a_v=_cat_cache(cache.v2a_v, v2a_v))
+    return vx, ax, new_cache
+
+
+class AVModel(nn.Module):
+    """The block stack with its timestep modulation and output heads
+    (causal_model.py:211-391 parameter names)."""
+
+    def __init__(self, cfg: AVConfig):
+        super().__init__()
+        self.cfg = cfg
+        vd, ad = cfg.video_dim, cfg.audio_dim
+        self.patchify_proj = nn.Linear(cfg.in_channels, vd)
+        self.audio_patchify_proj = nn.Linear(cfg.in_channels, ad)
+        self.adaln_single = AdaLayerNormSingle(vd, 6)
+        self.audio_adaln_single = AdaLayerNormSingle(ad, 6)
+        self.av_ca_video_scale_shift_adaln_single = AdaLayerNormSingle(vd, 4)
+        self.av_ca_audio_scale_shift_adaln_single = AdaLayerNormSingle(ad, 4)
+        self.av_ca_a2v_gate_adaln_single = AdaLayerNormSingle(vd, 1)
+        self.av_ca_v2a_gate_adaln_single = AdaLayerNormSingle(ad, 1)
+        self.transformer_blocks = nn.ModuleList([AVBlock(cfg) for _ in range(cfg.num_layers)])
+        self.scale_shift_table = nn.Parameter(torch.empty(2, vd))
+        self.norm_out = nn.LayerNorm(vd, elementwise_affine=False, eps=1e-6)
+        self.proj_out = nn.Linear(vd, cfg.out_channels)
+        self.audio_scale_shift_table = nn.Parameter(torch.empty(2, ad))
+        self.audio_norm_out = nn.LayerNorm(ad, elementwise_affine=False, eps=1e-6)
+        self.audio_proj_out = nn.Linear(ad, cfg.out_channels)
+
+    def _timestep(self, sigma: torch.Tensor, adaln: AdaLayerNormSingle, batch: int, dtype):
+        """causal_model.py:426-455."""
+        ts, emb = adaln((sigma * self.cfg.timestep_scale_multiplier).flatten(), dtype)
+        return ts.view(batch, -1, ts.shape[-1]), emb.view(batch, -1, emb.shape[-1])
+
+    def _cross_timestep(self, sigma: torch.Tensor, ss: AdaLayerNormSingle, gate: AdaLayerNormSingle, batch: int,
+                        dtype):
+        """causal_model.py:457-496."""
+        scaled = (sigma * self.cfg.timestep_scale_multiplier).flatten()
+        factor = self.cfg.av_ca_timestep_scale_multiplier / self.cfg.timestep_scale_multiplier
+        s, _ = ss(scaled, dtype)
+        g, _ = gate(scaled * factor, dtype)
+        return s.view(batch, -1, s.shape[-1]), g.view(batch, -1, g.shape[-1])
+
+    @staticmethod
+    def _process_output(table, norm, proj, x, emb):
+        """causal_model.py:568-599."""
+        v = table[None, None].to(device=x.device, dtype=x.dtype) + emb[:, :, None]
+        shift, scale = v[:, :, 0], v[:, :, 1]
+        return proj(norm(x) * (1 + scale) + shift)
+
+    def forward_chunk(self, video_latent: torch.Tensor, audio_latent: torch.Tensor, sigma: torch.Tensor,
+                      video_ctx: torch.Tensor, audio_ctx: torch.Tensor, video_mask: Optional[torch.Tensor],
+                      audio_mask: Optional[torch.Tensor], video_pe, audio_pe, video_cross_pe, audio_cross_pe,
+                      caches: List[LayerKVCache], commit: bool = False):
+        """One denoising step of a chunk (the block loop of
+        model_forward_inference, kv_cache.py:2681-3365): returns the video and
+        audio outputs [B, T, out_channels] and, with ``commit``, the caches
+        with the chunk's keys appended (a denoise step leaves them as given)."""
+        B = video_latent.shape[0]
+        dt = self.patchify_proj.weight.dtype
+        vx = self.patchify_proj(video_latent)
+        ax = self.audio_patchify_proj(audio_latent)
+        v_ts, v_emb = self._timestep(sigma, self.adaln_single, B, dt)
+        a_ts, a_emb = self._timestep(sigma, self.audio_adaln_single, B, dt)
+        v_ss, v_gate = self._cross_timestep(sigma, self.av_ca_video_scale_shift_adaln_single,
+                                            self.av_ca_a2v_gate_adaln_single, B, dt)
+        a_ss, a_gate = self._cross_timestep(sigma, self.av_ca_audio_scale_shift_adaln_single,
+                                            self.av_ca_v2a_gate_adaln_single, B, dt)
+        new_caches = []
+        for blk, cache in zip(self.transformer_blocks, caches):
+            vx, ax, nc = block_forward_with_cache(blk, vx, ax, v_ts, a_ts, video_pe, audio_pe, video_cross_pe,
+                                                  audio_cross_pe, video_ctx, audio_ctx, video_mask, audio_mask,
+                                                  v_ss, v_gate, a_ss, a_gate, cache)
+            new_caches.append(nc if commit else cache)
+            del nc
+        vo = self._process_output(self.scale_shift_table, self.norm_out, self.proj_out, vx, v_emb)
+        ao = self._process_output(self.audio_scale_shift_table, self.audio_norm_out, self.audio_proj_out, ax, a_emb)
+        return vo, ao, new_caches
+
+
+def init_random_(model: nn.Module, seed: int, std: float = 0.02) -> None:
+    """Seeded random weights in place: linear weights ~N(0, std^2), biases 0,
+    modulation tables ~N(0, 1)/sqrt(width) (the reference's table init)."""
+    dev = next(model.parameters()).device
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if name.endswith("bias"):
+                p.zero_()
+            elif "scale_shift_table" in name:
+                p.copy_(torch.randn(p.shape, generator=g, device=dev) / math.sqrt(p.shape[-1]))
+            elif name.endswith("norm.weight"):
+                p.fill_(1.0)
+            else:
+                p.copy_(torch.randn(p.shape, generator=g, device=dev) * std)
+
+
+def build_model(cfg: AVConfig, device, seed: int = 3, dtype=torch.bfloat16) -> AVModel:
+    """The model constructed directly on ``device`` in ``dtype`` (no host copy
+    of the weights), then seeded."""
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(dtype)
+    try:
+        with torch.device(device):
+            m = AVModel(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    init_random_(m, seed)
+    return m.eval()

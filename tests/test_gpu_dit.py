@@ -1,0 +1,100 @@
+"""GPU parity of the dual-stream block stack (AdaLN-modulated video self,
+video text, audio self, audio text, A2V, V2A attention and the GELU FFNs,
+timestep modulation and output heads) against the fp32 oracle restatement,
+at a reduced width: 2 blocks, video 8 x 64 heads, audio 4 x 64 heads, a
+4x6 latent grid, 3-frame chunk over 6 cached frames, 10 audio tokens over 40
+cached, 16 text tokens with the last 4 masked, B = 2."""
+import pytest
+import torch
+
+from oracle import attention as OA
+from oracle import dit as OD
+from oracle import rope as OR
+import taomate_amd as T
+from taomate_amd import dit as D
+from taomate_amd.kv_cache import KVSpanView
+
+from .helpers import cosine
+
+pytestmark = pytest.mark.gpu
+
+CFG = D.AVConfig(num_layers=2, video_dim=512, audio_dim=256, video_heads=8, audio_heads=4, video_d_head=64,
+                 audio_d_head=64)
+B, GH, GW, NF, F0, NCACHE_F = 2, 4, 6, 3, 6, 6
+LA, LA_CACHE, A0, LT = 10, 40, 60, 16
+
+
+def _inputs():
+    g = torch.Generator().manual_seed(33)
+    r = lambda *s: torch.randn(*s, generator=g).to(torch.bfloat16).float()
+    hw = GH * GW
+    vd, ad = CFG.video_dim, CFG.audio_dim
+    x = dict(video=r(B, NF * hw, CFG.in_channels), audio=r(B, LA, CFG.in_channels),
+             sigma=torch.rand(B, generator=g), vctx=r(B, LT, vd), actx=r(B, LT, ad))
+    keep = torch.ones(B, LT, dtype=torch.int64)
+    keep[:, -4:] = 0
+    x["mask"] = OA.prepare_attention_mask(keep, torch.bfloat16)
+    x["cache"] = [dict(video_self_k=r(B, NCACHE_F * hw, CFG.video_heads, CFG.video_d_head),
+                       video_self_v=r(B, NCACHE_F * hw, CFG.video_heads, CFG.video_d_head),
+                       audio_self_k=r(B, LA_CACHE, CFG.audio_heads, CFG.audio_d_head),
+                       audio_self_v=r(B, LA_CACHE, CFG.audio_heads, CFG.audio_d_head))
+                  for _ in range(CFG.num_layers)]
+    return x
+
+
+def _pes(dev=None):
+    """(video, audio, video cross, audio cross) RoPE tables; oracle when dev is None."""
+    vd, cross = CFG.video_dim, CFG.audio_heads * CFG.audio_d_head
+    hw = GH * GW
+    if dev is None:
+        pe = lambda grid, dim, heads, f0, audio=False: OR.causal_precompute_freqs_cis(
+            grid, dim, start_frame=f0, num_attention_heads=heads, batch=B, is_audio=audio)
+    else:
+        pe = lambda grid, dim, heads, f0, audio=False: T.causal_precompute_freqs_cis(
+            torch.tensor([list(grid)] * B), dim, start_frame=f0, device=dev, dtype=torch.bfloat16,
+            num_attention_heads=heads, is_audio=audio)
+    vcross = [t.repeat_interleave(hw, dim=2).contiguous() for t in pe((NF,), cross, CFG.audio_heads, F0)]
+    return (pe((NF, GH, GW), vd, CFG.video_heads, F0), pe((LA,), CFG.audio_dim, CFG.audio_heads, A0, True),
+            vcross, pe((LA,), cross, CFG.audio_heads, A0, True))
+
+
+def test_block_stack_matches_oracle(dev):
+    model = D.build_model(CFG, dev, seed=3)
+    params = {n: p.detach().float().cpu() for n, p in model.named_parameters()}
+    x = _inputs()
+    ref_v, ref_a = OD.forward_chunk(params, CFG, x["video"], x["audio"], x["sigma"], x["vctx"], x["actx"],
+                                    x["mask"].float(), x["mask"].float(), *_pes(), x["cache"])
+    hw = GH * GW
+    specs = {"video_self": T.ArenaSpec((NCACHE_F + NF) * hw, CFG.video_heads, CFG.video_d_head),
+             "audio_self": T.ArenaSpec(LA_CACHE + LA + 8, CFG.audio_heads, CFG.audio_d_head)}
+    kvc = T.init_kv_cache(CFG.num_layers, B, specs, dev)
+    caches = []
+    for lay, c in zip(kvc.layers, x["cache"]):
+        va, aa = lay.video_self_k.arena, lay.audio_self_k.arena
+        nv, na = c["video_self_k"].shape[1], c["audio_self_k"].shape[1]
+        va.slots("k", 0, nv).copy_(c["video_self_k"].to(dev, torch.bfloat16))
+        va.slots("v", 0, nv).copy_(c["video_self_v"].to(dev, torch.bfloat16))
+        aa.slots("k", 0, na).copy_(c["audio_self_k"].to(dev, torch.bfloat16))
+        aa.slots("v", 0, na).copy_(c["audio_self_v"].to(dev, torch.bfloat16))
+        caches.append(T.LayerKVCache(video_self_k=KVSpanView(va, "k", [(0, nv)]),
+                                     video_self_v=KVSpanView(va, "v", [(0, nv)]),
+                                     audio_self_k=KVSpanView(aa, "k", [(0, na)]),
+                                     audio_self_v=KVSpanView(aa, "v", [(0, na)])))
+    bf = lambda t: t.to(dev, torch.bfloat16)
+    with torch.no_grad():
+        vo, ao, kept = model.forward_chunk(bf(x["video"]), bf(x["audio"]), x["sigma"].to(dev), bf(x["vctx"]),
+                                           bf(x["actx"]), bf(x["mask"]), bf(x["mask"]), *_pes(dev), caches)
+        # a committed step appends the chunk's keys to every self-attention cache
+        _, _, committed = model.forward_chunk(bf(x["video"]), bf(x["audio"]), x["sigma"].to(dev),
+                                              bf(x["vctx"]), bf(x["actx"]), bf(x["mask"]), bf(x["mask"]),
+                                              *_pes(dev), caches, commit=True)
+    torch.cuda.synchronize()
+    assert kept is not caches and all(k is c for k, c in zip(kept, caches))
+    assert committed[0].video_self_k.shape[1] == (NCACHE_F + NF) * hw
+    assert committed[1].audio_self_k.shape[1] == LA_CACHE + LA
+    assert torch.isfinite(vo).all() and torch.isfinite(ao).all()
+    cv, ca = cosine(vo, ref_v), cosine(ao, ref_a)
+    assert cv >= 0.999 and ca >= 0.999, (cv, ca)
+    for out, ref in ((vo, ref_v), (ao, ref_a)):
+        err = (out.float().cpu() - ref).abs().max().item()
+        assert err <= 3e-2 * ref.abs().max().item(), err

@@ -14,7 +14,8 @@ plus the new chunk.  Activations are bf16, as on the reference's GPU path.
 """
 from __future__ import annotations
 
-from typing import List, Optional, Tuple
+import weakref
+from typing import Dict, List, Optional, Tuple
 
 import torch
 import torch.nn as nn
@@ -142,6 +143,47 @@ def _key_padding_mask(mask: Optional[torch.Tensor], B: int, Lk: int) -> Optional
     return m.to(torch.float32).contiguous()
 
 
+# A key-padding mask whose kept keys are the same prefix in every batch row,
+# with every other key at or below -1e30 (the reference's (m - 1) * finfo.max
+# form), gives those keys a weight of exactly 0 in float32: attending the
+# prefix alone is the same computation.  The check needs the mask's values on
+# the host, so its result is kept per mask tensor (dropped when the tensor
+# dies, recomputed after an in-place change) and a mask reused across blocks
+# and steps costs one synchronisation.
+_PREFIX: Dict[int, Tuple[int, Optional[int]]] = {}
+
+
+def _kept_prefix(mask: torch.Tensor, km: torch.Tensor) -> Optional[int]:
+    key = id(mask)
+    hit = _PREFIX.get(key)
+    if hit is not None and hit[0] == mask._version:
+        return hit[1]
+    kept, dropped = km == 0, km <= -1e30
+    n: Optional[int] = None
+    if bool((kept | dropped).all()):
+        counts = kept.sum(dim=1)
+        n0 = int(counts[0])
+        if n0 > 0 and bool((counts == n0).all()) and bool(kept[:, :n0].all()):
+            n = n0
+    if hit is None:
+        weakref.finalize(mask, _PREFIX.pop, key, None)
+    _PREFIX[key] = (mask._version, n)
+    return n
+
+
+def _key_major(v: torch.Tensor) -> torch.Tensor:
+    """V [B, L, H, D] copied into a key-major store [B, H, D, L rounded up to 8]
+    (zero tail), returned as its [B, L, H, D] view: the layout the pipelined
+    kernel streams straight into LDS."""
+    B, L, H, D = v.shape
+    store = torch.empty(B, H, D, -(-L // 8) * 8, dtype=v.dtype, device=v.device)
+    if store.shape[-1] > L:
+        store[..., L:].zero_()
+    view = store.permute(0, 3, 1, 2)[:, :L]
+    kernels.kv_append(v, view)
+    return view
+
+
 def standard_attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                mask: Optional[torch.Tensor] = None,
                                scale: Optional[float] = None) -> torch.Tensor:
@@ -155,6 +197,13 @@ def standard_attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
         kk = kk.contiguous()
         vv = vv.contiguous()
     km = _key_padding_mask(mask, q.shape[0], k.shape[1])
+    if km is not None:
+        n = _kept_prefix(mask, km)
+        if n is not None:
+            kk, vv, km = kk[:, :n], vv[:, :n], None
+    B, Lq, H, D = qq.shape
+    if km is None and D in (64, 128) and Lq >= 256 and kk.shape[1] >= 64:
+        vv = _key_major(vv)
     kernels.flash_attn(qq, [KVSegment(kk, vv)], out, key_mask=km, scale=scale)
     return out
 

@@ -220,3 +220,38 @@ def test_denoise_steps_do_not_commit(dev):
     assert full.shape[1] == 7 * hw
     assert cosine(full[:, 4 * hw:], rk) >= 0.9999
     assert cosine(full[:, :4 * hw], ck) >= 0.9999
+
+
+@pytest.mark.parametrize("kind", ["common_prefix", "per_row_prefix", "holes", "soft_bias", "bool_prefix"])
+def test_standard_attention_mask_forms(dev, kind):
+    """Key-padding masks through standard_attention_forward: a prefix kept in
+    every row is attended as the prefix alone (pipelined kernel on a key-major
+    V copy); other forms (row-dependent prefixes, holes, finite biases) take the
+    masked kernel.  All against the oracle with the same additive mask."""
+    B, Lq, Lk, H, D = 2, 384, 700, 8, 128
+    g = torch.Generator().manual_seed(61)
+    q = torch.randn(B, Lq, H, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Lk, H, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Lk, H, D, generator=g).to(torch.bfloat16)
+    keep = torch.ones(B, Lk, dtype=torch.int64)
+    if kind in ("common_prefix", "bool_prefix"):
+        keep[:, 555:] = 0
+    elif kind == "per_row_prefix":
+        keep[0, 555:] = 0
+        keep[1, 610:] = 0
+    elif kind == "holes":
+        keep[:, 100:180] = 0
+        keep[1, 400:] = 0
+    if kind == "soft_bias":
+        add = (torch.randn(B, 1, 1, Lk, generator=g) * 2.0).to(torch.bfloat16)
+    else:
+        add = OA.prepare_attention_mask(keep, torch.bfloat16)
+    ref = OA.standard_attention_forward(q.float(), k.float(), v.float(), add.float())
+    m = keep.bool().view(B, 1, 1, Lk).to(dev) if kind == "bool_prefix" else add.to(dev)
+    with torch.no_grad():
+        out = T.standard_attention_forward(q.to(dev), k.to(dev), v.to(dev), mask=m)
+        again = T.standard_attention_forward(q.to(dev), k.to(dev), v.to(dev), mask=m)  # cached decision
+    torch.cuda.synchronize()
+    assert_bf16_close(out, ref, kind)
+    assert torch.equal(out, again)
+    assert cosine(out, ref) >= 0.9999

@@ -206,6 +206,26 @@ int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t H, int64_t 
  */
 int ltx_flash_attn_workspace_size(int64_t B, int64_t Lq, int64_t H, int64_t D, int64_t* bytes);
 
+/*
+ * Gated residual update and AdaLN-modulated RMSNorm, bf16 [B, L, C] rows.
+ * Replaces the bf16 tensor-op chains of block_forward_with_cache
+ * (ltx_causal/transformer/kv_cache.py:2194-2633) around each attention and
+ * feed-forward: x' = x + y * gate (x + y without a gate; x when y is null),
+ * then n = rms_norm(x') * (1 + scale) + shift (rms_norm of
+ * ltx_causal/transformer/causal_block.py:94-101; plain rms_norm(x') without
+ * scale/shift), rounding to bf16 where the reference's tensor ops do.
+ *   Every tensor is given by a pointer and (batch, row) element strides with
+ *   the C channels contiguous; gate/scale/shift rows are per batch element
+ *   (row stride 0) or per row.  x_out (may equal x) receives x' when y is
+ *   given; n_out (may be null) receives n.  C must be a multiple of 8, at
+ *   most 8192; rows 16-byte aligned.
+ */
+int ltx_adaln(int64_t B, int64_t L, int64_t C, const void* x, int64_t x_bs, int64_t x_ls,
+              const void* y, int64_t y_bs, int64_t y_ls, const void* gate, int64_t g_bs, int64_t g_ls,
+              void* x_out, int64_t xo_bs, int64_t xo_ls, void* n_out, int64_t n_bs, int64_t n_ls,
+              const void* scale, int64_t s_bs, int64_t s_ls, const void* shift, int64_t h_bs,
+              int64_t h_ls, float eps, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,8 @@ SIGNATURES = {
                            _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _ptr, _ptr, _i64, _i64,
                            _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _ptr, _f32, _ptr, _i64, _ptr],
     "ltx_flash_attn_workspace_size": [_i64, _i64, _i64, _i64, _ptr],
+    "ltx_adaln": [_i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64,
+                  _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _f32, _ptr],
 }
 
 

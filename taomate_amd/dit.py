@@ -16,9 +16,10 @@ line up:
 
 Built: the shipped inference configuration (no text-cross AdaLN, no gated
 attention, no learned memory adapters, captions already at the model width as
-in the 22B checkpoints).  The q/k/v/out projections, FFNs and AdaLN are
-PyTorch-ROCm GEMMs and elementwise ops; every attention (video self, text
-cross, audio self, text cross, A2V, V2A) runs through this package's kernels.
+in the 22B checkpoints).  The q/k/v/out projections, FFNs and the timestep
+MLPs are PyTorch-ROCm GEMMs; every attention (video self, text cross, audio
+self, text cross, A2V, V2A) and every residual update + (modulated) RMSNorm
+pair between them runs through this package's kernels.
 """
 from __future__ import annotations
 
@@ -30,6 +31,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import kernels
 from .attention import CausalLTXAttention, attention_with_cache
 from .kv_cache import LayerKVCache, _cat_cache
 
@@ -158,6 +160,23 @@ class AVBlock(nn.Module):
         return (*ss, *gate)
 
 
+def _modulate(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, eps: float) -> torch.Tensor:
+    """rms_norm(x) * (1 + scale) + shift in one pass (ltx_adaln)."""
+    n = torch.empty_like(x)
+    kernels.adaln(x, n_out=n, scale=scale, shift=shift, eps=eps)
+    return n
+
+
+def _residual(x: torch.Tensor, y: torch.Tensor, gate: Optional[torch.Tensor] = None, norm: bool = False,
+              scale: Optional[torch.Tensor] = None, shift: Optional[torch.Tensor] = None, eps: float = 1e-6):
+    """x + y * gate (x + y without a gate) and, with ``norm``, the next input
+    rms_norm(x') [* (1 + scale) + shift] in the same pass (ltx_adaln)."""
+    xo = torch.empty_like(x)
+    n = torch.empty_like(x) if norm else None
+    kernels.adaln(x, y=y, gate=gate, x_out=xo, n_out=n, scale=scale, shift=shift, eps=eps)
+    return xo, n
+
+
 def block_forward_with_cache(block: AVBlock, vx: torch.Tensor, ax: torch.Tensor, v_ts: torch.Tensor,
                              a_ts: torch.Tensor, video_pe, audio_pe, video_cross_pe, audio_cross_pe,
                              video_ctx: torch.Tensor, audio_ctx: torch.Tensor, video_mask: Optional[torch.Tensor],
@@ -165,43 +184,48 @@ def block_forward_with_cache(block: AVBlock, vx: torch.Tensor, ax: torch.Tensor,
                              a_cross_ss: torch.Tensor, a_cross_gate: torch.Tensor, cache: LayerKVCache):
     """kv_cache.py:2145-2656 (synchronous branch): video self -> video text ->
     audio self -> audio text -> A2V -> V2A -> video FFN -> audio FFN.
-    Returns (vx, ax, cache with the chunk's K/V appended)."""
+    Returns (vx, ax, cache with the chunk's K/V appended).
+
+    The residual updates and the (modulated) RMSNorms between the attentions
+    and FFNs are fused pairwise into ltx_adaln passes with the reference's
+    bf16 rounding; each stream's text residual is applied before the
+    cross-modal norms as in the reference (the audio stream does not read the
+    video residual before that point, so the order of the two streams'
+    updates does not matter)."""
     eps = block.norm_eps
     B = vx.shape[0]
-    # video self-attention
+    # video self-attention, then its residual fused with the text-cross norm
     sh, sc, g = block.get_ada_values(block.scale_shift_table, B, v_ts, slice(0, 3))
-    out, vs_k, vs_v = attention_with_cache(block.attn1, rms_norm(vx, eps) * (1 + sc) + sh, None, video_pe, None,
+    out, vs_k, vs_v = attention_with_cache(block.attn1, _modulate(vx, sc, sh, eps), None, video_pe, None,
                                            cache.video_self_k, cache.video_self_v)
-    vx = vx + out * g
-    # video text cross-attention (kv_cache.py:1134-1141, no prompt AdaLN)
-    vx = vx + block.attn2(rms_norm(vx, eps), context=video_ctx, mask=video_mask)
-    # audio self-attention
+    vx, vn = _residual(vx, out, g, norm=True, eps=eps)
+    v_text = block.attn2(vn, context=video_ctx, mask=video_mask)   # kv_cache.py:1134-1141
+    # audio self-attention and text cross-attention
     sh, sc, g = block.get_ada_values(block.audio_scale_shift_table, B, a_ts, slice(0, 3))
-    out, as_k, as_v = attention_with_cache(block.audio_attn1, rms_norm(ax, eps) * (1 + sc) + sh, None, audio_pe,
-                                           None, cache.audio_self_k, cache.audio_self_v)
-    ax = ax + out * g
-    ax = ax + block.audio_attn2(rms_norm(ax, eps), context=audio_ctx, mask=audio_mask)
+    out, as_k, as_v = attention_with_cache(block.audio_attn1, _modulate(ax, sc, sh, eps), None, audio_pe, None,
+                                           cache.audio_self_k, cache.audio_self_v)
+    ax, an = _residual(ax, out, g, norm=True, eps=eps)
+    a_text = block.audio_attn2(an, context=audio_ctx, mask=audio_mask)
+    vx, _ = _residual(vx, v_text, eps=eps)
+    ax, _ = _residual(ax, a_text, eps=eps)
     # cross-modal: both read the norms taken before either update
-    vn, an = rms_norm(vx, eps), rms_norm(ax, eps)
     sc_a_a2v, sh_a_a2v, sc_a_v2a, sh_a_v2a, gate_v2a = block.get_av_ca_ada_values(
         block.scale_shift_table_a2v_ca_audio, B, a_cross_ss, a_cross_gate)
     sc_v_a2v, sh_v_a2v, sc_v_v2a, sh_v_v2a, gate_a2v = block.get_av_ca_ada_values(
         block.scale_shift_table_a2v_ca_video, B, v_cross_ss, v_cross_gate)
-    vx_a2v = vn * (1 + sc_v_a2v) + sh_v_a2v
-    ax_a2v = an * (1 + sc_a_a2v) + sh_a_a2v
-    ax_v2a = an * (1 + sc_a_v2a) + sh_a_v2a
-    vx_v2a = vn * (1 + sc_v_v2a) + sh_v_v2a
-    a2v, a2v_k, a2v_v = attention_with_cache(block.audio_to_video_attn, vx_a2v, ax_a2v, video_cross_pe,
+    a2v, a2v_k, a2v_v = attention_with_cache(block.audio_to_video_attn, _modulate(vx, sc_v_a2v, sh_v_a2v, eps),
+                                             _modulate(ax, sc_a_a2v, sh_a_a2v, eps), video_cross_pe,
                                              audio_cross_pe, cache.a2v_k, cache.a2v_v)
-    vx = vx + a2v * gate_a2v
-    v2a, v2a_k, v2a_v = attention_with_cache(block.video_to_audio_attn, ax_v2a, vx_v2a, audio_cross_pe,
+    v2a, v2a_k, v2a_v = attention_with_cache(block.video_to_audio_attn, _modulate(ax, sc_a_v2a, sh_a_v2a, eps),
+                                             _modulate(vx, sc_v_v2a, sh_v_v2a, eps), audio_cross_pe,
                                              video_cross_pe, cache.v2a_k, cache.v2a_v)
-    ax = ax + v2a * gate_v2a
-    # feed-forward
+    # cross-modal residuals fused with the feed-forward input norms
     sh, sc, g = block.get_ada_values(block.scale_shift_table, B, v_ts, slice(3, 6))
-    vx = vx + block.ff(rms_norm(vx, eps) * (1 + sc) + sh) * g
+    vx, vn = _residual(vx, a2v, gate_a2v, norm=True, scale=sc, shift=sh, eps=eps)
+    vx, _ = _residual(vx, block.ff(vn), g, eps=eps)
     sh, sc, g = block.get_ada_values(block.audio_scale_shift_table, B, a_ts, slice(3, 6))
-    ax = ax + block.audio_ff(rms_norm(ax, eps) * (1 + sc) + sh) * g
+    ax, an = _residual(ax, v2a, gate_v2a, norm=True, scale=sc, shift=sh, eps=eps)
+    ax, _ = _residual(ax, block.audio_ff(an), g, eps=eps)
     new_cache = LayerKVCache(
         video_self_k=_cat_cache(cache.video_self_k, vs_k), video_self_v=_cat_cache(cache.video_self_v, vs_v),
         audio_self_k=_cat_cache(cache.audio_self_k, as_k), audio_self_v=_cat_cache(cache.audio_self_v, as_v),

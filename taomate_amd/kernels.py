@@ -323,3 +323,34 @@ def flash_attn(q: torch.Tensor, segments: List[KVSegment], out: torch.Tensor,
            int(frame_tokens), _ptr(key_mask), mask_bs, out.data_ptr(), out.stride(0), out.stride(1),
            out.stride(2), _ptr(lse), float(scale) if scale is not None else 0.0, _ptr(ws), ws_bytes,
            _stream(q))
+
+
+def adaln(x: torch.Tensor, y: Optional[torch.Tensor] = None, gate: Optional[torch.Tensor] = None,
+          x_out: Optional[torch.Tensor] = None, n_out: Optional[torch.Tensor] = None,
+          scale: Optional[torch.Tensor] = None, shift: Optional[torch.Tensor] = None, eps: float = 1e-6) -> None:
+    """ltx_adaln on bf16 [B, L, C] rows: x_out = x + y * gate (x + y without a
+    gate), n_out = rms_norm(x_out or x) * (1 + scale) + shift (plain rms_norm
+    without scale/shift).  gate/scale/shift are [B, 1 or L, C]."""
+    _need_gpu(x, y, gate, x_out, n_out, scale, shift)
+    if x.dim() != 3 or x.dtype != torch.bfloat16:
+        raise ValueError("adaln: x must be bf16 [B, L, C]")
+    B, L, C = x.shape
+
+    def rows(t, name, per_row_ok=True):
+        if t is None:
+            return None, 0, 0
+        if t.dtype != torch.bfloat16 or t.dim() != 3 or t.shape[0] != B or t.shape[2] != C or t.stride(2) != 1:
+            raise ValueError(f"adaln: {name} must be bf16 [B, L or 1, C] with contiguous channels")
+        if t.shape[1] == L:
+            return t.data_ptr(), t.stride(0), (t.stride(1) if L > 1 else 0)
+        if t.shape[1] == 1 and per_row_ok:
+            return t.data_ptr(), t.stride(0), 0
+        raise ValueError(f"adaln: {name} rows {t.shape[1]} vs L={L}")
+
+    args = [rows(x, "x"), rows(y, "y"), rows(gate, "gate"), rows(x_out, "x_out"), rows(n_out, "n_out"),
+            rows(scale, "scale"), rows(shift, "shift")]
+    for t, name in ((y, "y"), (x_out, "x_out"), (n_out, "n_out")):
+        if t is not None and t.shape[1] != L:
+            raise ValueError(f"adaln: {name} must have L={L} rows")
+    flat = [v for a in args for v in a]
+    N.call("ltx_adaln", B, L, C, *flat, float(eps), _stream(x))

@@ -479,3 +479,34 @@ def test_flash_attn_fp8_ragged_segments(dev, D, scales):
         assert cosine(out, _ref_attn(q, K, V)) >= FP8_COSINE
     assert_bf16_close(out, _ref_attn(q, torch.cat(kd, 1), torch.cat(vd, 1)), f"fp8 ragged {scales} D{D}",
                       max_abs=2e-2 * max(scales), mean_abs=2e-3 * max(scales))
+
+
+@pytest.mark.parametrize("C,L,per_row", [(4096, 1152, False), (2048, 75, True), (512, 33, False)])
+def test_adaln_matches_torch_ops(dev, C, L, per_row):
+    """ltx_adaln against the reference's bf16 tensor ops on the GPU: the gated
+    residual x + y * g is bit-identical; rms_norm(x') * (1 + scale) + shift
+    rounds the same way (equal except where the float32 sum of squares, summed
+    in another order, flips a rounding)."""
+    g = gen(21)
+    B = 2
+    x = randn((B, L, C), g, torch.bfloat16, 2.0).to(dev)
+    y = randn((B, L, C), g, torch.bfloat16, 0.5).to(dev)
+    rows = L if per_row else 1
+    tab = randn((B, rows, 3, C), g, torch.bfloat16, 0.3).to(dev)   # shift / scale / gate rows, strided
+    sh, sc, gt = tab.unbind(dim=2)
+    F = torch.nn.functional
+    x1 = x + y * gt
+    ref_mod = F.rms_norm(x1, (C,), None, 1e-6) * (1 + sc) + sh
+    ref_plain = F.rms_norm(x1, (C,), None, 1e-6)
+    xo, n1, n2 = torch.empty_like(x), torch.empty_like(x), torch.empty_like(x)
+    kernels.adaln(x, y=y, gate=gt, x_out=xo, n_out=n1, scale=sc, shift=sh)
+    kernels.adaln(x, y=y, gate=gt, x_out=x, n_out=n2)        # in place, plain norm
+    r = torch.empty_like(x)
+    kernels.adaln(xo, y=y, x_out=r)                           # ungated residual only
+    torch.cuda.synchronize()
+    assert torch.equal(xo, x1) and torch.equal(x, x1)
+    assert torch.equal(r, x1 + y)
+    for out, ref in ((n1, ref_mod), (n2, ref_plain)):
+        exact = (out == ref).float().mean().item()
+        d = (out.float() - ref.float()).abs().max().item()
+        assert exact >= 0.995 and d <= 2 ** -6 * ref.float().abs().max().item(), (exact, d)

@@ -466,8 +466,8 @@ def main():
                    "heads": H, "head_dim": D, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": ach, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": ach / PEAK_BF16_TFLOPS, "traffic": measured_traffic(args.kv),
-                     "kernel": ("flash_fwd_pipe_kernel<128> + flash_combine_kernel<128>" if args.kv == "bf16"
-                                else "flash_fwd_kernel<128, fp8> + flash_combine_kernel<128>"),
+                     "kernel": ("flash_fwd_pipe_kernel<128, false> + flash_combine_kernel<128>" if args.kv == "bf16"
+                                else "flash_fwd_pipe_kernel<128, true> + flash_combine_kernel<128>"),
                      "kernel_ms": ms_attn,
                      "algorithmic_flops": fl, "algorithmic_bytes": attn_bytes(kvb)},
         "attention_tflops": ach,

@@ -1132,16 +1132,17 @@ int launch_flash(const FlashParams& p, hipStream_t st) {
 using namespace ltx;
 
 // Resident workgroups the device holds for this kernel (CUs x occupancy),
-// cached per device.
-template <typename K>
-int resident_slots(K kernel, int threads = 256) {
-  static int cache[64][2];  // [device] -> {valid, slots}, per kernel
+// cached per device; one cache per kernel (each instantiation of the
+// template has its own).
+template <auto Kernel>
+int resident_slots(int threads = 256) {
+  static int cache[64][2];  // [device] -> {valid, slots}
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   if (!cache[dev][0]) {
     int cus = 0, occ = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, threads, 0) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, Kernel, threads, 0) != hipSuccess) return 0;
     cache[dev][1] = cus * (occ > 0 ? occ : 1);
     cache[dev][0] = 1;
   }
@@ -1173,17 +1174,38 @@ inline int64_t workspace_bytes_for(int64_t tail, int split, int64_t D) {
   return tail * split * kBM * (2 * 4 + D * 2);  // (max, sum) fp32 + bf16 O row
 }
 
+// Resident slots of the kernel a call with head size D takes: the pipelined
+// kernel for key-major bf16 V (vkey) or fp8 K/V, else the staged kernel
+// (its masked instance for a key mask).
+inline int flash_slots(int64_t D, bool vkey, bool fp8, bool mask) {
+  if (D == 128)
+    return vkey   ? resident_slots<flash_fwd_pipe_kernel<128, false>>()
+           : fp8  ? resident_slots<flash_fwd_pipe_kernel<128, true>>()
+           : mask ? resident_slots<flash_fwd_kernel<128, false, true>>()
+                  : resident_slots<flash_fwd_kernel<128, false, false>>();
+  return vkey   ? resident_slots<flash_fwd_pipe_kernel<64, false>>()
+         : fp8  ? resident_slots<flash_fwd_pipe_kernel<64, true>>()
+         : mask ? resident_slots<flash_fwd_kernel<64, false, true>>()
+                : resident_slots<flash_fwd_kernel<64, false, false>>();
+}
+
 extern "C" int ltx_flash_attn_workspace_size(int64_t B, int64_t Lq, int64_t H, int64_t D,
                                              int64_t* bytes) {
   clear_error();
   LTX_REQUIRE(bytes != nullptr && B >= 1 && H >= 1 && Lq >= 0 && (D == 64 || D == 128),
               "ltx_flash_attn_workspace_size: bad arguments");
-  const int slots = resident_slots(flash_fwd_kernel<128, false, false>);
+  // the largest partial buffer any of the kernels for this D may plan
   const int64_t nq = B * H * ((Lq + kBM - 1) / kBM);
-  int64_t n_full;
-  int split;
-  plan_split(nq, 1 << 30, slots, &n_full, &split);
-  *bytes = split > 1 ? workspace_bytes_for(nq - n_full, kMaxSplit, D) : 0;
+  int64_t need = 0;
+  for (int k = 0; k < 4; ++k) {
+    const int slots = flash_slots(D, k == 1, k == 2, k == 3);
+    int64_t n_full;
+    int split;
+    plan_split(nq, 1 << 30, slots, &n_full, &split);
+    const int64_t b = split > 1 ? workspace_bytes_for(nq - n_full, kMaxSplit, D) : 0;
+    need = b > need ? b : need;
+  }
+  *bytes = need;
   return LTX_OK;
 }
 
@@ -1285,9 +1307,7 @@ extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t 
     int64_t n_full = nq;
     int split = 1;
     if (workspace != nullptr) {
-      const int slots = vkey ? resident_slots(flash_fwd_pipe_kernel<128, false>)
-                        : fp8  ? resident_slots(flash_fwd_pipe_kernel<128, true>)
-                               : resident_slots(flash_fwd_kernel<128, false, false>);
+      const int slots = flash_slots(D, vkey, fp8, key_mask != nullptr);
       plan_split(nq, p.tile_start[n], slots, &n_full, &split);
       if (split > 1 && workspace_bytes_for(nq - n_full, split, D) > workspace_bytes) {
         n_full = nq;

@@ -201,7 +201,7 @@ def stream_bench(dev, n_chunks: int = 60, kv_dtype: str = "fp8", warm_chunks: in
                         "window | current chunk, whole layer per chunk (projections included)"}
 
 
-def dit_bench(dev, steps: int = 5, warmup: int = 2):
+def dit_bench(dev, steps: int = 5, warmup: int = 2, learned_memory: bool = False):
     """One denoising step of the 48-block dual-stream model (video 32 x 128,
     d = 4096; audio 32 x 64, d = 2048; 4x GELU FFNs; AdaLN modulation) for one
     512x768 chunk at B = 2: 1152 video tokens over the 3456 cached keys of the
@@ -209,14 +209,17 @@ def dit_bench(dev, steps: int = 5, warmup: int = 2):
     (20 % masked) for both streams, A2V / V2A over the chunk's own tokens.
     Random bf16 weights (seed 3), sigma ~ U(0, 1).  Timed with HIP events
     around whole steps; the attention share is the summed duration of every
-    attention call (events around each, same stream) over the step time."""
+    attention call (events around each, same stream) over the step time.
+    With ``learned_memory`` every 4th block carries the memory adapters
+    (video 8 x 64 over 48 tokens + colour FiLM, audio 8 x 32 over 64 tokens),
+    fed by a StreamingMemory updated once with the chunk's latents."""
     from taomate_amd import dit as Dm
     from taomate_amd import kernels
     import taomate_amd as T
     from taomate_amd.kv_cache import KVSpanView
     from taomate_amd.rope import causal_precompute_freqs_cis
 
-    cfg = Dm.AVConfig()
+    cfg = Dm.AVConfig(learned_memory_enabled=learned_memory, learned_memory_color_film_enabled=learned_memory)
     model = Dm.build_model(cfg, dev, seed=3)
     n_params = sum(p.numel() for p in model.parameters())
     g = torch.Generator(device=dev)
@@ -260,8 +263,17 @@ def dit_bench(dev, steps: int = 5, warmup: int = 2):
         e1.record()
         attn_events.append((e0, e1))
 
+    mem = {}
+    if learned_memory:
+        state = T.StreamingMemory()
+        lat5 = vlat.view(B, 3, GRID_H, GRID_W, cfg.in_channels).permute(0, 1, 4, 2, 3)
+        state.set_reference(lat5, alat)
+        state.update(lat5, alat)
+        mem = state.with_conditional_memory({}, device=dev, dtype=torch.bfloat16)
+
     def step():
-        return model.forward_chunk(vlat, alat, sigma, vctx, actx, mask, mask, vpe, ape, vcross, across, caches)
+        return model.forward_chunk(vlat, alat, sigma, vctx, actx, mask, mask, vpe, ape, vcross, across, caches,
+                                   **mem)
 
     with torch.no_grad():
         for _ in range(warmup):
@@ -289,10 +301,11 @@ def dit_bench(dev, steps: int = 5, warmup: int = 2):
         ms_attn = sum(a.elapsed_time(b) for a, b in attn_events)
     res = {"ms_per_step": ms, "chunk_query_tokens_per_s": B * LQ / (ms * 1e-3), "params": n_params,
            "attention_ms": ms_attn, "attention_share": ms_attn / ms_inst, "attention_calls": len(attn_events),
-           "outputs_finite": finite,
+           "outputs_finite": finite, "learned_memory": learned_memory,
            "workload": "48 dual-stream blocks (video 32x128 d=4096, audio 32x64 d=2048, 4x GELU FFNs, AdaLN), "
                        "one denoising step of a 512x768 chunk at B=2: 1152 video queries over 3456 cached + 1152 "
-                       "keys, 75 audio over 600 + 75, 1024 text keys (20% masked), A2V 1152x75, V2A 75x1152"}
+                       "keys, 75 audio over 600 + 75, 1024 text keys (20% masked), A2V 1152x75, V2A 75x1152"
+                       + ("; memory adapters on every 4th block" if learned_memory else "")}
     del model, caches, kvc
     torch.cuda.empty_cache()
     return res
@@ -369,6 +382,8 @@ def main():
     ap.add_argument("--stream-only", action="store_true", help="run only the 60-chunk long-stream measurement")
     ap.add_argument("--no-dit", action="store_true", help="skip the 48-block denoising-step measurement")
     ap.add_argument("--dit-only", action="store_true", help="run only the 48-block denoising-step measurement")
+    ap.add_argument("--dit-learned-memory", action="store_true",
+                    help="the 48-block step with learned-memory adapters on every 4th block")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 256 MiB device copy (scale reference for HBM byte counters)")
     ap.add_argument("--copy-bandwidth", action="store_true",
@@ -392,7 +407,7 @@ def main():
         print(json.dumps(stream_bench(dev)))
         return
     if args.dit_only:
-        print(json.dumps(dit_bench(dev)))
+        print(json.dumps(dit_bench(dev, learned_memory=args.dit_learned_memory)))
         return
     if args.copy_bandwidth:
         for mib in (64, 256, 1024, 4096):
@@ -481,7 +496,7 @@ def main():
     if not args.no_stream:
         res["long_stream"] = stream_bench(dev)
     if not args.no_dit:
-        res["dit_step"] = dit_bench(dev)
+        res["dit_step"] = dit_bench(dev, learned_memory=args.dit_learned_memory)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(res))

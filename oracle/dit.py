@@ -8,6 +8,9 @@ Follows, op for op:
   block_forward_with_cache (sync branch)   ltx_causal/transformer/kv_cache.py:2145-2656
   text cross-attention without prompt AdaLN  kv_cache.py:1134-1141
   _process_output                          causal_model.py:568-599
+  learned-memory adapters (optional)       causal_block.py:108-193, 489-505;
+                                           placement kv_cache.py:2217-2330;
+                                           encoders kv_cache.py:529-559
 with the attention calls of ``oracle.attention`` (attention_with_cache for
 self / cross-modal attention, text_cross_attention for the text keys).
 Weights are plain dicts of float32 CPU tensors keyed by the reference's
@@ -71,28 +74,86 @@ def feed_forward(p: Dict[str, torch.Tensor], prefix: str, x: torch.Tensor) -> to
     return F.linear(h, p[prefix + "net.2.weight"], p[prefix + "net.2.bias"])
 
 
+def memory_attention(p: Dict[str, torch.Tensor], prefix: str, x: torch.Tensor, memory: torch.Tensor,
+                     heads: int) -> torch.Tensor:
+    """LearnedMemoryAttention.forward (causal_block.py:136-160): q from x,
+    k / v from the memory tokens, SDPA with scale 1/sqrt(head), out linear."""
+    if memory.shape[0] == 1 and x.shape[0] > 1:
+        memory = memory.expand(x.shape[0], -1, -1)
+    q = F.linear(x, p[prefix + "to_q.weight"])
+    k = F.linear(memory, p[prefix + "to_k.weight"])
+    v = F.linear(memory, p[prefix + "to_v.weight"])
+    B, L, md = q.shape
+    d = md // heads
+    split = lambda t: t.reshape(B, t.shape[1], heads, d)
+    out = OA.standard_attention_forward(split(q), split(k), split(v), scale=1.0 / math.sqrt(d))
+    return F.linear(out.reshape(B, L, md), p[prefix + "to_out.weight"], p[prefix + "to_out.bias"])
+
+
+def color_film(p: Dict[str, torch.Tensor], prefix: str, x: torch.Tensor, color: torch.Tensor) -> torch.Tensor:
+    """LearnedMemoryColorFiLM.forward (causal_block.py:179-193)."""
+    if color.shape[0] == 1 and x.shape[0] > 1:
+        color = color.expand(x.shape[0], -1)
+    h = F.silu(F.linear(color, p[prefix + "net.0.weight"], p[prefix + "net.0.bias"]))
+    scale, shift = F.linear(h, p[prefix + "net.2.weight"], p[prefix + "net.2.bias"]).chunk(2, dim=-1)
+    return x * scale[:, None] + shift[:, None]
+
+
+def _memory_steps(p, prefix, cfg, stream: str, memory, color):
+    """The adapters of one stream in this block, as (callable, argument) pairs."""
+    if prefix + f"{stream}_memory_attn.to_q.weight" not in p:
+        return []
+    steps = []
+    if memory is not None:
+        steps.append((lambda x, m: memory_attention(p, prefix + f"{stream}_memory_attn.", x, m,
+                                                    cfg.learned_memory_heads), memory))
+    if stream == "video" and color is not None and prefix + "video_color_film.net.0.weight" in p:
+        steps.append((lambda x, c: color_film(p, prefix + "video_color_film.", x, c), color))
+    return steps
+
+
+def _apply_steps(x, steps, eps):
+    """x + adapter(rms_norm(x), arg) for each step (causal_block.py:489-505)."""
+    for fn, arg in steps:
+        x = x + fn(rms_norm(x, eps), arg)
+    return x
+
+
 def block_forward(p: Dict[str, torch.Tensor], prefix: str, cfg, vx, ax, v_ts, a_ts, video_pe, audio_pe,
                   video_cross_pe, audio_cross_pe, video_ctx, audio_ctx, video_mask, audio_mask, v_ss, v_gate,
-                  a_ss, a_gate, cache: Dict[str, Optional[torch.Tensor]]):
+                  a_ss, a_gate, cache: Dict[str, Optional[torch.Tensor]], video_memory=None, audio_memory=None,
+                  color_memory=None):
     """kv_cache.py:2145-2656, synchronous branch.  ``cache`` holds dense
     video_self_k/v, audio_self_k/v, a2v_k/v, v2a_k/v (or None).  Returns (vx, ax)."""
     eps = cfg.norm_eps
     B = vx.shape[0]
     vh, vdh, ah, adh = cfg.video_heads, cfg.video_d_head, cfg.audio_heads, cfg.audio_d_head
+    mode = getattr(cfg, "learned_memory_mode", None)
+    v_steps = _memory_steps(p, prefix, cfg, "video", video_memory, color_memory)
+    a_steps = _memory_steps(p, prefix, cfg, "audio", audio_memory, None)
     t = lambda n: p[prefix + n]
     sh, sc, g = ada_values(t("scale_shift_table"), B, v_ts, slice(0, 3))
     out, _, _ = OA.attention_with_cache(attn_weights(p, prefix + "attn1.", vh, vdh), rms_norm(vx, eps) * (1 + sc) + sh,
                                         None, video_pe, None, cache.get("video_self_k"), cache.get("video_self_v"))
     vx = vx + out * g
-    vx = vx + OA.text_cross_attention(attn_weights(p, prefix + "attn2.", vh, vdh), rms_norm(vx, eps), video_ctx,
-                                      video_mask)
+    if mode == "memory_kv_side_branch":
+        vx = _apply_steps(vx, v_steps, eps)
+    v_text = OA.text_cross_attention(attn_weights(p, prefix + "attn2.", vh, vdh), rms_norm(vx, eps), video_ctx,
+                                     video_mask)
     sh, sc, g = ada_values(t("audio_scale_shift_table"), B, a_ts, slice(0, 3))
     out, _, _ = OA.attention_with_cache(attn_weights(p, prefix + "audio_attn1.", ah, adh),
                                         rms_norm(ax, eps) * (1 + sc) + sh, None, audio_pe, None,
                                         cache.get("audio_self_k"), cache.get("audio_self_v"))
     ax = ax + out * g
-    ax = ax + OA.text_cross_attention(attn_weights(p, prefix + "audio_attn2.", ah, adh), rms_norm(ax, eps),
-                                      audio_ctx, audio_mask)
+    if mode == "memory_kv_side_branch":
+        ax = _apply_steps(ax, a_steps, eps)
+    a_text = OA.text_cross_attention(attn_weights(p, prefix + "audio_attn2.", ah, adh), rms_norm(ax, eps),
+                                     audio_ctx, audio_mask)
+    vx = vx + v_text
+    ax = ax + a_text
+    if mode == "cross_attn_adapter":
+        vx = _apply_steps(vx, v_steps, eps)
+        ax = _apply_steps(ax, a_steps, eps)
     vn, an = rms_norm(vx, eps), rms_norm(ax, eps)
     sc_a_a2v, sh_a_a2v, sc_a_v2a, sh_a_v2a, gate_v2a = av_ca_values(t("scale_shift_table_a2v_ca_audio"), B, a_ss,
                                                                      a_gate)
@@ -115,7 +176,8 @@ def block_forward(p: Dict[str, torch.Tensor], prefix: str, cfg, vx, ax, v_ts, a_
 
 def forward_chunk(p: Dict[str, torch.Tensor], cfg, video_latent, audio_latent, sigma, video_ctx, audio_ctx,
                   video_mask, audio_mask, video_pe, audio_pe, video_cross_pe, audio_cross_pe,
-                  caches: List[Dict[str, Optional[torch.Tensor]]]) -> Tuple[torch.Tensor, torch.Tensor]:
+                  caches: List[Dict[str, Optional[torch.Tensor]]], learned_memory_video=None,
+                  learned_memory_audio=None, learned_memory_color=None) -> Tuple[torch.Tensor, torch.Tensor]:
     """One denoising step: patchify, timestep modulation (causal_model.py:426-496),
     the block loop, the output heads (causal_model.py:568-599)."""
     B = video_latent.shape[0]
@@ -129,13 +191,23 @@ def forward_chunk(p: Dict[str, torch.Tensor], cfg, video_latent, audio_latent, s
     a_ss, _ = adaln_single(p, "av_ca_audio_scale_shift_adaln_single.", s)
     v_gate, _ = adaln_single(p, "av_ca_a2v_gate_adaln_single.", s * factor)
     a_gate, _ = adaln_single(p, "av_ca_v2a_gate_adaln_single.", s * factor)
+    vm = am = cm = None
+    if getattr(cfg, "learned_memory_enabled", False):
+        if learned_memory_video is not None:
+            vm = F.linear(learned_memory_video, p["learned_memory_video_encoder.weight"],
+                          p["learned_memory_video_encoder.bias"])
+        if learned_memory_audio is not None:
+            am = F.linear(learned_memory_audio, p["learned_memory_audio_encoder.weight"],
+                          p["learned_memory_audio_encoder.bias"])
+        if learned_memory_color is not None and cfg.learned_memory_color_film_enabled:
+            cm = learned_memory_color
     view = lambda x: x.view(B, -1, x.shape[-1])
     v_ts, v_emb, a_ts, a_emb = view(v_ts), view(v_emb), view(a_ts), view(a_emb)
     v_ss, a_ss, v_gate, a_gate = view(v_ss), view(a_ss), view(v_gate), view(a_gate)
     for i in range(cfg.num_layers):
         vx, ax = block_forward(p, f"transformer_blocks.{i}.", cfg, vx, ax, v_ts, a_ts, video_pe, audio_pe,
                                video_cross_pe, audio_cross_pe, video_ctx, audio_ctx, video_mask, audio_mask,
-                               v_ss, v_gate, a_ss, a_gate, caches[i])
+                               v_ss, v_gate, a_ss, a_gate, caches[i], vm, am, cm)
 
     def head(table, proj, x, emb):
         v = table[None, None] + emb[:, :, None]

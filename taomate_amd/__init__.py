@@ -11,6 +11,8 @@ The public names mirror the reference's drop-in surface:
   (ltx_causal/transformer/kv_cache.py:321-398, ltx_causal/wrapper.py:15)
 * ``retain_streaming_context``, ``cache_segments``, ``attach_segments``
   (taomate/inference/cache.py), ``compute_av_blocks`` (mask_builder.py:102)
+* ``LearnedMemoryState``, ``StreamingMemory`` (taomate/runtime_support/learned_memory.py,
+  taomate/inference/memory.py)
 
 All device math goes through ``lib/libtaomate_ltx.so`` (C ABI in
 ``include/taomate_ltx.h``); importing works without it, the first kernel call
@@ -25,6 +27,7 @@ from .kv_cache import (ArenaSpec, KVArena, KVArenaFull, KVCache, KVSpanView, Lay
                        _cat_cache, init_kv_cache)
 from .rope import CausalRopeType, apply_split_rotary_emb, causal_precompute_freqs_cis, generate_freq_grid
 from .streaming import ChunkStream, retain_pinned_recent
+from .memory import LearnedMemoryState, StreamingMemory
 from . import dit
 
 __all__ = [
@@ -34,4 +37,5 @@ __all__ = [
     "retain_streaming_context", "ArenaSpec", "KVArena", "KVArenaFull", "KVCache", "KVSpanView",
     "LayerKVCache", "_cat_cache", "init_kv_cache", "CausalRopeType", "apply_split_rotary_emb",
     "causal_precompute_freqs_cis", "generate_freq_grid", "ChunkStream", "retain_pinned_recent",
+    "LearnedMemoryState", "StreamingMemory",
 ]

@@ -15,8 +15,12 @@ line up:
   _process_output                     causal_model.py:568-599
 
 Built: the shipped inference configuration (no text-cross AdaLN, no gated
-attention, no learned memory adapters, captions already at the model width as
-in the 22B checkpoints).  The q/k/v/out projections, FFNs and the timestep
+attention, captions already at the model width as in the 22B checkpoints),
+with the learned long-memory adapters as an option (``AVConfig.learned_memory_*``):
+  LearnedMemoryAttention / ColorFiLM  causal_block.py:108-193
+  their placement in the block        kv_cache.py:2217-2330 (_apply_learned_memory,
+                                      causal_block.py:489-505)
+  memory encoders                     causal_model.py:253-268, kv_cache.py:529-559  The q/k/v/out projections, FFNs and the timestep
 MLPs are PyTorch-ROCm GEMMs; every attention (video self, text cross, audio
 self, text cross, A2V, V2A) and every residual update + (modulated) RMSNorm
 pair between them runs through this package's kernels.
@@ -32,7 +36,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import kernels
-from .attention import CausalLTXAttention, attention_with_cache
+from .attention import CausalLTXAttention, attention_with_cache, standard_attention_forward
 from .kv_cache import LayerKVCache, _cat_cache
 
 
@@ -119,13 +123,84 @@ class AVConfig:
     norm_eps: float = 1e-6
     timestep_scale_multiplier: float = 1000.0
     av_ca_timestep_scale_multiplier: float = 1.0
+    # learned long-memory adapters (causal_model.py:194-203), off by default
+    learned_memory_enabled: bool = False
+    learned_memory_mode: str = "cross_attn_adapter"   # or "memory_kv_side_branch"
+    learned_memory_layer_interval: int = 4
+    learned_memory_video_dim: int = 512
+    learned_memory_audio_dim: int = 256
+    learned_memory_heads: int = 8
+    learned_memory_color_film_enabled: bool = False
+    learned_memory_color_condition_dim: int = 512
+    learned_memory_color_film_hidden_dim: int = 256
+
+
+class LearnedMemoryAttention(nn.Module):
+    """Cross-attention of the stream's tokens over the memory tokens
+    (causal_block.py:108-160): q from the stream (query_dim -> memory_dim),
+    k / v from the memory, ``heads`` heads of memory_dim / heads, out back to
+    query_dim.  The attention runs on the flash kernels; a head size of 32
+    (the audio adapter's 256 / 8) is zero-padded to 64, which leaves q.k and
+    the first 32 output columns unchanged."""
+
+    def __init__(self, query_dim: int, memory_dim: int, heads: int):
+        super().__init__()
+        heads = max(1, int(heads))
+        if memory_dim % heads != 0:
+            raise ValueError(f"learned memory dim ({memory_dim}) must be divisible by heads ({heads})")
+        self.heads = heads
+        self.head_dim = memory_dim // heads
+        if self.head_dim not in (32, 64, 128):
+            raise ValueError(f"learned memory head size {self.head_dim} is not built (32, 64 or 128)")
+        self.to_q = nn.Linear(query_dim, memory_dim, bias=False)
+        self.to_k = nn.Linear(memory_dim, memory_dim, bias=False)
+        self.to_v = nn.Linear(memory_dim, memory_dim, bias=False)
+        self.to_out = nn.Linear(memory_dim, query_dim, bias=True)
+
+    def forward(self, x: torch.Tensor, memory: Optional[torch.Tensor]) -> torch.Tensor:
+        if memory is None or memory.numel() == 0:
+            return x.new_zeros(x.shape)
+        B, L, _ = x.shape
+        if memory.shape[0] == 1 and B > 1:
+            memory = memory.expand(B, -1, -1)
+        memory = memory.to(device=x.device, dtype=x.dtype)
+        h, d = self.heads, self.head_dim
+        q = self.to_q(x).view(B, L, h, d)
+        k = self.to_k(memory).view(B, memory.shape[1], h, d)
+        v = self.to_v(memory).view(B, memory.shape[1], h, d)
+        if d == 32:
+            pad = lambda t: F.pad(t, (0, 32))
+            q, k, v = pad(q), pad(k), pad(v)
+        out = standard_attention_forward(q, k, v, scale=1.0 / math.sqrt(d))
+        return self.to_out(out[..., :d].reshape(B, L, h * d))
+
+
+class LearnedMemoryColorFiLM(nn.Module):
+    """x * scale + shift from the colour-memory vector through a SiLU MLP
+    (causal_block.py:163-193)."""
+
+    def __init__(self, condition_dim: int, query_dim: int, hidden_dim: int):
+        super().__init__()
+        self.net = nn.Sequential(nn.Linear(int(condition_dim), max(1, int(hidden_dim))), nn.SiLU(),
+                                 nn.Linear(max(1, int(hidden_dim)), query_dim * 2))
+
+    def forward(self, x: torch.Tensor, color: Optional[torch.Tensor]) -> torch.Tensor:
+        if color is None or color.numel() == 0:
+            return x.new_zeros(x.shape)
+        if color.shape[0] == 1 and x.shape[0] > 1:
+            color = color.expand(x.shape[0], -1)
+        scale, shift = self.net(color.to(device=x.device, dtype=x.dtype)).chunk(2, dim=-1)
+        return x * scale.unsqueeze(1) + shift.unsqueeze(1)
 
 
 class AVBlock(nn.Module):
-    """Parameters of CausalAVTransformerBlock (causal_block.py:211-376), same names."""
+    """Parameters of CausalAVTransformerBlock (causal_block.py:211-376), same
+    names; block ``idx`` carries the memory adapters when learned memory is on
+    and (idx + 1) is a multiple of the layer interval (causal_model.py:341-359)."""
 
-    def __init__(self, cfg: AVConfig):
+    def __init__(self, cfg: AVConfig, idx: int = 0):
         super().__init__()
+        self.idx = idx
         vd, ad = cfg.video_dim, cfg.audio_dim
         self.norm_eps = cfg.norm_eps
         self.attn1 = CausalLTXAttention(vd, heads=cfg.video_heads, dim_head=cfg.video_d_head, norm_eps=cfg.norm_eps)
@@ -145,6 +220,19 @@ class AVBlock(nn.Module):
                                                       dim_head=cfg.audio_d_head, norm_eps=cfg.norm_eps)
         self.scale_shift_table_a2v_ca_audio = nn.Parameter(torch.empty(5, ad))
         self.scale_shift_table_a2v_ca_video = nn.Parameter(torch.empty(5, vd))
+        memory_here = (cfg.learned_memory_enabled and cfg.learned_memory_layer_interval > 0
+                       and (idx + 1) % cfg.learned_memory_layer_interval == 0)
+        self.learned_memory_mode = str(cfg.learned_memory_mode) if memory_here else None
+        if memory_here and self.learned_memory_mode not in ("cross_attn_adapter", "memory_kv_side_branch"):
+            raise ValueError(f"learned_memory_mode must be cross_attn_adapter or memory_kv_side_branch, "
+                             f"got {self.learned_memory_mode!r}")
+        self.video_memory_attn = LearnedMemoryAttention(vd, cfg.learned_memory_video_dim,
+                                                        cfg.learned_memory_heads) if memory_here else None
+        self.audio_memory_attn = LearnedMemoryAttention(ad, cfg.learned_memory_audio_dim,
+                                                        cfg.learned_memory_heads) if memory_here else None
+        self.video_color_film = LearnedMemoryColorFiLM(
+            cfg.learned_memory_color_condition_dim, vd, cfg.learned_memory_color_film_hidden_dim) \
+            if memory_here and cfg.learned_memory_color_film_enabled else None
 
     @staticmethod
     def get_ada_values(table: torch.Tensor, batch: int, timestep: torch.Tensor, idx: slice):
@@ -177,11 +265,29 @@ def _residual(x: torch.Tensor, y: torch.Tensor, gate: Optional[torch.Tensor] = N
     return xo, n
 
 
+def _apply_memory(x: torch.Tensor, n: Optional[torch.Tensor], steps, eps: float, need_norm: bool):
+    """x + adapter(rms_norm(x), arg) for each (adapter, arg) in ``steps``
+    (causal_block.py:489-505), each residual fused with the next norm.  ``n``
+    is rms_norm(x) when already known.  Returns (x, rms_norm(x) or None)."""
+    steps = [(m, a) for m, a in steps if m is not None and a is not None]
+    for i, (mod, arg) in enumerate(steps):
+        if n is None:
+            n = torch.empty_like(x)
+            kernels.adaln(x, n_out=n, eps=eps)
+        x, n = _residual(x, mod(n, arg), norm=need_norm or i + 1 < len(steps), eps=eps)
+    if need_norm and n is None:
+        n = torch.empty_like(x)
+        kernels.adaln(x, n_out=n, eps=eps)
+    return x, n
+
+
 def block_forward_with_cache(block: AVBlock, vx: torch.Tensor, ax: torch.Tensor, v_ts: torch.Tensor,
                              a_ts: torch.Tensor, video_pe, audio_pe, video_cross_pe, audio_cross_pe,
                              video_ctx: torch.Tensor, audio_ctx: torch.Tensor, video_mask: Optional[torch.Tensor],
                              audio_mask: Optional[torch.Tensor], v_cross_ss: torch.Tensor, v_cross_gate: torch.Tensor,
-                             a_cross_ss: torch.Tensor, a_cross_gate: torch.Tensor, cache: LayerKVCache):
+                             a_cross_ss: torch.Tensor, a_cross_gate: torch.Tensor, cache: LayerKVCache,
+                             video_memory: Optional[torch.Tensor] = None, audio_memory: Optional[torch.Tensor] = None,
+                             color_memory: Optional[torch.Tensor] = None):
     """kv_cache.py:2145-2656 (synchronous branch): video self -> video text ->
     audio self -> audio text -> A2V -> V2A -> video FFN -> audio FFN.
     Returns (vx, ax, cache with the chunk's K/V appended).
@@ -191,23 +297,42 @@ def block_forward_with_cache(block: AVBlock, vx: torch.Tensor, ax: torch.Tensor,
     bf16 rounding; each stream's text residual is applied before the
     cross-modal norms as in the reference (the audio stream does not read the
     video residual before that point, so the order of the two streams'
-    updates does not matter)."""
+    updates does not matter).
+
+    With memory adapters (``block.learned_memory_mode``): the video memory
+    attention and colour FiLM, and the audio memory attention, are applied
+    after the streams' self-attention residuals ("memory_kv_side_branch") or
+    after their text residuals ("cross_attn_adapter"), kv_cache.py:2217-2330."""
     eps = block.norm_eps
     B = vx.shape[0]
+    mode = getattr(block, "learned_memory_mode", None)
+    v_steps = ((getattr(block, "video_memory_attn", None), video_memory),
+               (getattr(block, "video_color_film", None), color_memory))
+    a_steps = ((getattr(block, "audio_memory_attn", None), audio_memory),)
+    side, after_text = mode == "memory_kv_side_branch", mode == "cross_attn_adapter"
+    v_mem = any(m is not None and a is not None for m, a in v_steps)
+    a_mem = any(m is not None and a is not None for m, a in a_steps)
     # video self-attention, then its residual fused with the text-cross norm
     sh, sc, g = block.get_ada_values(block.scale_shift_table, B, v_ts, slice(0, 3))
     out, vs_k, vs_v = attention_with_cache(block.attn1, _modulate(vx, sc, sh, eps), None, video_pe, None,
                                            cache.video_self_k, cache.video_self_v)
     vx, vn = _residual(vx, out, g, norm=True, eps=eps)
+    if side:
+        vx, vn = _apply_memory(vx, vn, v_steps, eps, need_norm=True)
     v_text = block.attn2(vn, context=video_ctx, mask=video_mask)   # kv_cache.py:1134-1141
     # audio self-attention and text cross-attention
     sh, sc, g = block.get_ada_values(block.audio_scale_shift_table, B, a_ts, slice(0, 3))
     out, as_k, as_v = attention_with_cache(block.audio_attn1, _modulate(ax, sc, sh, eps), None, audio_pe, None,
                                            cache.audio_self_k, cache.audio_self_v)
     ax, an = _residual(ax, out, g, norm=True, eps=eps)
+    if side:
+        ax, an = _apply_memory(ax, an, a_steps, eps, need_norm=True)
     a_text = block.audio_attn2(an, context=audio_ctx, mask=audio_mask)
-    vx, _ = _residual(vx, v_text, eps=eps)
-    ax, _ = _residual(ax, a_text, eps=eps)
+    vx, vn = _residual(vx, v_text, norm=after_text and v_mem, eps=eps)
+    ax, an = _residual(ax, a_text, norm=after_text and a_mem, eps=eps)
+    if after_text:
+        vx, _ = _apply_memory(vx, vn, v_steps, eps, need_norm=False)
+        ax, _ = _apply_memory(ax, an, a_steps, eps, need_norm=False)
     # cross-modal: both read the norms taken before either update
     sc_a_a2v, sh_a_a2v, sc_a_v2a, sh_a_v2a, gate_v2a = block.get_av_ca_ada_values(
         block.scale_shift_table_a2v_ca_audio, B, a_cross_ss, a_cross_gate)
@@ -250,7 +375,13 @@ class AVModel(nn.Module):
         self.av_ca_audio_scale_shift_adaln_single = AdaLayerNormSingle(ad, 4)
         self.av_ca_a2v_gate_adaln_single = AdaLayerNormSingle(vd, 1)
         self.av_ca_v2a_gate_adaln_single = AdaLayerNormSingle(ad, 1)
-        self.transformer_blocks = nn.ModuleList([AVBlock(cfg) for _ in range(cfg.num_layers)])
+        self.transformer_blocks = nn.ModuleList([AVBlock(cfg, i) for i in range(cfg.num_layers)])
+        if cfg.learned_memory_enabled:   # causal_model.py:253-268
+            self.learned_memory_video_encoder = nn.Linear(cfg.in_channels, cfg.learned_memory_video_dim)
+            self.learned_memory_audio_encoder = nn.Linear(cfg.in_channels, cfg.learned_memory_audio_dim)
+        else:
+            self.learned_memory_video_encoder = None
+            self.learned_memory_audio_encoder = None
         self.scale_shift_table = nn.Parameter(torch.empty(2, vd))
         self.norm_out = nn.LayerNorm(vd, elementwise_affine=False, eps=1e-6)
         self.proj_out = nn.Linear(vd, cfg.out_channels)
@@ -282,13 +413,28 @@ class AVModel(nn.Module):
     def forward_chunk(self, video_latent: torch.Tensor, audio_latent: torch.Tensor, sigma: torch.Tensor,
                       video_ctx: torch.Tensor, audio_ctx: torch.Tensor, video_mask: Optional[torch.Tensor],
                       audio_mask: Optional[torch.Tensor], video_pe, audio_pe, video_cross_pe, audio_cross_pe,
-                      caches: List[LayerKVCache], commit: bool = False):
+                      caches: List[LayerKVCache], commit: bool = False,
+                      learned_memory_video: Optional[torch.Tensor] = None,
+                      learned_memory_audio: Optional[torch.Tensor] = None,
+                      learned_memory_color: Optional[torch.Tensor] = None):
         """One denoising step of a chunk (the block loop of
         model_forward_inference, kv_cache.py:2681-3365): returns the video and
         audio outputs [B, T, out_channels] and, with ``commit``, the caches
-        with the chunk's keys appended (a denoise step leaves them as given)."""
+        with the chunk's keys appended (a denoise step leaves them as given).
+        The learned-memory tensors ([B, N, in_channels] tokens, [B, 4C] colour
+        vector, from ``LearnedMemoryState.with_conditional_memory``) are used
+        when the model has memory adapters."""
         B = video_latent.shape[0]
         dt = self.patchify_proj.weight.dtype
+        vm = am = cm = None
+        if self.cfg.learned_memory_enabled:   # kv_cache.py:529-559
+            dev = video_latent.device
+            if learned_memory_video is not None:
+                vm = self.learned_memory_video_encoder(learned_memory_video.to(device=dev, dtype=dt))
+            if learned_memory_audio is not None:
+                am = self.learned_memory_audio_encoder(learned_memory_audio.to(device=dev, dtype=dt))
+            if learned_memory_color is not None and self.cfg.learned_memory_color_film_enabled:
+                cm = learned_memory_color.to(device=dev, dtype=dt)
         vx = self.patchify_proj(video_latent)
         ax = self.audio_patchify_proj(audio_latent)
         v_ts, v_emb = self._timestep(sigma, self.adaln_single, B, dt)
@@ -301,7 +447,7 @@ class AVModel(nn.Module):
         for blk, cache in zip(self.transformer_blocks, caches):
             vx, ax, nc = block_forward_with_cache(blk, vx, ax, v_ts, a_ts, video_pe, audio_pe, video_cross_pe,
                                                   audio_cross_pe, video_ctx, audio_ctx, video_mask, audio_mask,
-                                                  v_ss, v_gate, a_ss, a_gate, cache)
+                                                  v_ss, v_gate, a_ss, a_gate, cache, vm, am, cm)
             new_caches.append(nc if commit else cache)
             del nc
         vo = self._process_output(self.scale_shift_table, self.norm_out, self.proj_out, vx, v_emb)

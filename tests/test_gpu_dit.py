@@ -98,3 +98,59 @@ def test_block_stack_matches_oracle(dev):
     for out, ref in ((vo, ref_v), (ao, ref_a)):
         err = (out.float().cpu() - ref).abs().max().item()
         assert err <= 3e-2 * ref.abs().max().item(), err
+
+
+@pytest.mark.parametrize("mode", ["cross_attn_adapter", "memory_kv_side_branch"])
+def test_block_stack_with_learned_memory_matches_oracle(dev, mode):
+    """The same stack with learned-memory adapters on block 1 (interval 2):
+    video memory attention (512 = 8 x 64) and colour FiLM, audio memory
+    attention (256 = 8 x 32, the zero-padded head path), in both placements;
+    48 video and 64 audio memory tokens, a 512-wide colour vector."""
+    cfg = D.AVConfig(num_layers=2, video_dim=512, audio_dim=256, video_heads=8, audio_heads=4, video_d_head=64,
+                     audio_d_head=64, learned_memory_enabled=True, learned_memory_mode=mode,
+                     learned_memory_layer_interval=2, learned_memory_color_film_enabled=True)
+    model = D.build_model(cfg, dev, seed=5)
+    assert model.transformer_blocks[1].video_memory_attn is not None
+    assert model.transformer_blocks[0].video_memory_attn is None
+    params = {n: p.detach().float().cpu() for n, p in model.named_parameters()}
+    x = _inputs()
+    g = torch.Generator().manual_seed(44)
+    mem = dict(learned_memory_video=torch.randn(B, 48, cfg.in_channels, generator=g),
+               learned_memory_audio=torch.randn(B, 64, cfg.in_channels, generator=g),
+               learned_memory_color=torch.randn(B, 512, generator=g) * 0.5)
+    mem = {k: v.to(torch.bfloat16).float() for k, v in mem.items()}
+    dense = lambda c: {k: v for k, v in c.items()}
+    ref_v, ref_a = OD.forward_chunk(params, cfg, x["video"], x["audio"], x["sigma"], x["vctx"], x["actx"],
+                                    x["mask"].float(), x["mask"].float(), *_pes(), [dense(c) for c in x["cache"]],
+                                    **mem)
+    hw = GH * GW
+    specs = {"video_self": T.ArenaSpec((NCACHE_F + NF) * hw, cfg.video_heads, cfg.video_d_head),
+             "audio_self": T.ArenaSpec(LA_CACHE + LA + 8, cfg.audio_heads, cfg.audio_d_head)}
+    kvc = T.init_kv_cache(cfg.num_layers, B, specs, dev)
+    caches = []
+    for lay, c in zip(kvc.layers, x["cache"]):
+        va, aa = lay.video_self_k.arena, lay.audio_self_k.arena
+        nv, na = c["video_self_k"].shape[1], c["audio_self_k"].shape[1]
+        va.slots("k", 0, nv).copy_(c["video_self_k"].to(dev, torch.bfloat16))
+        va.slots("v", 0, nv).copy_(c["video_self_v"].to(dev, torch.bfloat16))
+        aa.slots("k", 0, na).copy_(c["audio_self_k"].to(dev, torch.bfloat16))
+        aa.slots("v", 0, na).copy_(c["audio_self_v"].to(dev, torch.bfloat16))
+        caches.append(T.LayerKVCache(video_self_k=KVSpanView(va, "k", [(0, nv)]),
+                                     video_self_v=KVSpanView(va, "v", [(0, nv)]),
+                                     audio_self_k=KVSpanView(aa, "k", [(0, na)]),
+                                     audio_self_v=KVSpanView(aa, "v", [(0, na)])))
+    bf = lambda t: t.to(dev, torch.bfloat16)
+    with torch.no_grad():
+        args = (bf(x["video"]), bf(x["audio"]), x["sigma"].to(dev), bf(x["vctx"]), bf(x["actx"]), bf(x["mask"]),
+                bf(x["mask"]), *_pes(dev), caches)
+        vo, ao, _ = model.forward_chunk(*args, **{k: bf(v) for k, v in mem.items()})
+        vo0, ao0, _ = model.forward_chunk(*args)
+    torch.cuda.synchronize()
+    assert torch.isfinite(vo).all() and torch.isfinite(ao).all()
+    cv, ca = cosine(vo, ref_v), cosine(ao, ref_a)
+    assert cv >= 0.999 and ca >= 0.999, (cv, ca)
+    for out, ref in ((vo, ref_v), (ao, ref_a)):
+        err = (out.float().cpu() - ref).abs().max().item()
+        assert err <= 3e-2 * ref.abs().max().item(), err
+    # the memory reached both streams
+    assert (vo - vo0).abs().max().item() > 1e-2 and (ao - ao0).abs().max().item() > 1e-2

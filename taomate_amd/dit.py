@@ -416,14 +416,17 @@ class AVModel(nn.Module):
                       caches: List[LayerKVCache], commit: bool = False,
                       learned_memory_video: Optional[torch.Tensor] = None,
                       learned_memory_audio: Optional[torch.Tensor] = None,
-                      learned_memory_color: Optional[torch.Tensor] = None):
+                      learned_memory_color: Optional[torch.Tensor] = None, kv_cache_only: bool = False):
         """One denoising step of a chunk (the block loop of
         model_forward_inference, kv_cache.py:2681-3365): returns the video and
         audio outputs [B, T, out_channels] and, with ``commit``, the caches
         with the chunk's keys appended (a denoise step leaves them as given).
         The learned-memory tensors ([B, N, in_channels] tokens, [B, 4C] colour
         vector, from ``LearnedMemoryState.with_conditional_memory``) are used
-        when the model has memory adapters."""
+        when the model has memory adapters.  ``kv_cache_only`` is the clean
+        commit pass (kv_cache.py:3302-3309): it commits and returns
+        (None, None, caches) without the output heads."""
+        commit = commit or kv_cache_only
         B = video_latent.shape[0]
         dt = self.patchify_proj.weight.dtype
         vm = am = cm = None
@@ -450,6 +453,8 @@ class AVModel(nn.Module):
                                                   v_ss, v_gate, a_ss, a_gate, cache, vm, am, cm)
             new_caches.append(nc if commit else cache)
             del nc
+        if kv_cache_only:
+            return None, None, new_caches
         vo = self._process_output(self.scale_shift_table, self.norm_out, self.proj_out, vx, v_emb)
         ao = self._process_output(self.audio_scale_shift_table, self.audio_norm_out, self.audio_proj_out, ax, a_emb)
         return vo, ao, new_caches

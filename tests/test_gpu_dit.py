@@ -65,8 +65,9 @@ def test_block_stack_matches_oracle(dev):
     ref_v, ref_a = OD.forward_chunk(params, CFG, x["video"], x["audio"], x["sigma"], x["vctx"], x["actx"],
                                     x["mask"].float(), x["mask"].float(), *_pes(), x["cache"])
     hw = GH * GW
-    specs = {"video_self": T.ArenaSpec((NCACHE_F + NF) * hw, CFG.video_heads, CFG.video_d_head),
-             "audio_self": T.ArenaSpec(LA_CACHE + LA + 8, CFG.audio_heads, CFG.audio_d_head)}
+    # room for two chunks past the cache: the committed step's and the clean commit pass's
+    specs = {"video_self": T.ArenaSpec((NCACHE_F + 2 * NF) * hw, CFG.video_heads, CFG.video_d_head),
+             "audio_self": T.ArenaSpec(LA_CACHE + 2 * LA + 8, CFG.audio_heads, CFG.audio_d_head)}
     kvc = T.init_kv_cache(CFG.num_layers, B, specs, dev)
     caches = []
     for lay, c in zip(kvc.layers, x["cache"]):
@@ -88,7 +89,13 @@ def test_block_stack_matches_oracle(dev):
         _, _, committed = model.forward_chunk(bf(x["video"]), bf(x["audio"]), x["sigma"].to(dev),
                                               bf(x["vctx"]), bf(x["actx"]), bf(x["mask"]), bf(x["mask"]),
                                               *_pes(dev), caches, commit=True)
+        # the clean commit pass: same caches, no outputs
+        nv_, na_, kv_only = model.forward_chunk(bf(x["video"]), bf(x["audio"]), torch.zeros_like(x["sigma"]).to(dev),
+                                                bf(x["vctx"]), bf(x["actx"]), bf(x["mask"]), bf(x["mask"]),
+                                                *_pes(dev), caches, kv_cache_only=True)
     torch.cuda.synchronize()
+    assert nv_ is None and na_ is None
+    assert kv_only[0].video_self_k.shape[1] == (NCACHE_F + NF) * hw
     assert kept is not caches and all(k is c for k, c in zip(kept, caches))
     assert committed[0].video_self_k.shape[1] == (NCACHE_F + NF) * hw
     assert committed[1].audio_self_k.shape[1] == LA_CACHE + LA

@@ -13,6 +13,8 @@ The public names mirror the reference's drop-in surface:
   (taomate/inference/cache.py), ``compute_av_blocks`` (mask_builder.py:102)
 * ``LearnedMemoryState``, ``StreamingMemory`` (taomate/runtime_support/learned_memory.py,
   taomate/inference/memory.py)
+* ``load_generator`` / ``save_generator`` (taomate/inference/model_runtime.py:182-425) and the
+  interactive prefix state (taomate/inference/streaming_runtime.py:1404-1500)
 
 All device math goes through ``lib/libtaomate_ltx.so`` (C ABI in
 ``include/taomate_ltx.h``); importing works without it, the first kernel call
@@ -29,6 +31,8 @@ from .rope import CausalRopeType, apply_split_rotary_emb, causal_precompute_freq
 from .streaming import ChunkStream, retain_pinned_recent
 from .memory import LearnedMemoryState, StreamingMemory
 from . import dit
+from .checkpoint import load_generator, save_generator
+from .prefix_state import build_prefix_state_payload, load_prefix_state, save_prefix_state
 
 __all__ = [
     "NativeCallError", "NativeLibraryError", "CausalLTXAttention", "attention_with_cache",
@@ -37,5 +41,6 @@ __all__ = [
     "retain_streaming_context", "ArenaSpec", "KVArena", "KVArenaFull", "KVCache", "KVSpanView",
     "LayerKVCache", "_cat_cache", "init_kv_cache", "CausalRopeType", "apply_split_rotary_emb",
     "causal_precompute_freqs_cis", "generate_freq_grid", "ChunkStream", "retain_pinned_recent",
-    "LearnedMemoryState", "StreamingMemory",
+    "LearnedMemoryState", "StreamingMemory", "load_generator", "save_generator", "build_prefix_state_payload",
+    "load_prefix_state", "save_prefix_state",
 ]

@@ -123,6 +123,7 @@ class AVConfig:
     norm_eps: float = 1e-6
     timestep_scale_multiplier: float = 1000.0
     av_ca_timestep_scale_multiplier: float = 1.0
+    apply_gated_attention: bool = False   # per-head output gates (to_gate_logits)
     # learned long-memory adapters (causal_model.py:194-203), off by default
     learned_memory_enabled: bool = False
     learned_memory_mode: str = "cross_attn_adapter"   # or "memory_kv_side_branch"
@@ -203,21 +204,25 @@ class AVBlock(nn.Module):
         self.idx = idx
         vd, ad = cfg.video_dim, cfg.audio_dim
         self.norm_eps = cfg.norm_eps
-        self.attn1 = CausalLTXAttention(vd, heads=cfg.video_heads, dim_head=cfg.video_d_head, norm_eps=cfg.norm_eps)
+        gated = cfg.apply_gated_attention
+        self.attn1 = CausalLTXAttention(vd, heads=cfg.video_heads, dim_head=cfg.video_d_head, norm_eps=cfg.norm_eps,
+                                        apply_gated_attention=gated)
         self.attn2 = CausalLTXAttention(vd, context_dim=vd, heads=cfg.video_heads, dim_head=cfg.video_d_head,
-                                        norm_eps=cfg.norm_eps)
+                                        norm_eps=cfg.norm_eps, apply_gated_attention=gated)
         self.ff = FeedForward(vd, vd)
         self.scale_shift_table = nn.Parameter(torch.empty(6, vd))
         self.audio_attn1 = CausalLTXAttention(ad, heads=cfg.audio_heads, dim_head=cfg.audio_d_head,
-                                              norm_eps=cfg.norm_eps)
+                                              norm_eps=cfg.norm_eps, apply_gated_attention=gated)
         self.audio_attn2 = CausalLTXAttention(ad, context_dim=ad, heads=cfg.audio_heads, dim_head=cfg.audio_d_head,
-                                              norm_eps=cfg.norm_eps)
+                                              norm_eps=cfg.norm_eps, apply_gated_attention=gated)
         self.audio_ff = FeedForward(ad, ad)
         self.audio_scale_shift_table = nn.Parameter(torch.empty(6, ad))
         self.audio_to_video_attn = CausalLTXAttention(vd, context_dim=ad, heads=cfg.audio_heads,
-                                                      dim_head=cfg.audio_d_head, norm_eps=cfg.norm_eps)
+                                                      dim_head=cfg.audio_d_head, norm_eps=cfg.norm_eps,
+                                                      apply_gated_attention=gated)
         self.video_to_audio_attn = CausalLTXAttention(ad, context_dim=vd, heads=cfg.audio_heads,
-                                                      dim_head=cfg.audio_d_head, norm_eps=cfg.norm_eps)
+                                                      dim_head=cfg.audio_d_head, norm_eps=cfg.norm_eps,
+                                                      apply_gated_attention=gated)
         self.scale_shift_table_a2v_ca_audio = nn.Parameter(torch.empty(5, ad))
         self.scale_shift_table_a2v_ca_video = nn.Parameter(torch.empty(5, vd))
         memory_here = (cfg.learned_memory_enabled and cfg.learned_memory_layer_interval > 0

@@ -116,7 +116,9 @@ def build_workload(dev, kv_dtype: str = "bf16"):
 
 
 def make_step(w):
-    """Returns (step, attn_only, norm_only, append_only) closures over the workload."""
+    """Returns (step, attn_only, norm_only, append_only, prep) closures over the
+    workload; prep is the step's first part: the fused q/k norm + RoPE + V
+    append launch (bf16 arena) or norm then the fp8 pair append."""
     from taomate_amd import kernels
     from taomate_amd.kernels import KVSegment
 
@@ -145,12 +147,20 @@ def make_step(w):
     def attn():
         kernels.flash_attn(q4, segs, w["out"], frame_tokens=frame)
 
+    def prep():
+        if a.fp8:
+            norm()
+            append()
+        else:
+            kernels.qk_rmsnorm_rope(w["q_lin"], w["q"], w["gq"], 1e-6, w["pe"], H, D,
+                                    w["k_lin"], kbf, w["gk"], 1e-6, w["pe"],
+                                    v_in=w["v_lin"].view(B, LQ, H, D), v_out=vd)
+
     def step():
-        norm()
-        append()
+        prep()
         attn()
 
-    return step, attn, norm, append
+    return step, attn, norm, append, prep
 
 
 def stream_bench(dev, n_chunks: int = 60, kv_dtype: str = "fp8", warm_chunks: int = 60):
@@ -313,7 +323,8 @@ def dit_bench(dev, steps: int = 5, warmup: int = 2, learned_memory: bool = False
 
 def time_region(fn, iters: int) -> float:
     """Average ms per call over `iters` back-to-back calls, HIP events on the
-    launching stream (profiling aid; the reported figures come from the timed
+    launching stream (the attention-only profiling mode and the standalone
+    rates of the norm and append kernels; the step figures come from the timed
     step loop)."""
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -422,7 +433,7 @@ def main():
             del x, y
         return
     w = build_workload(dev, args.kv)
-    step, attn, norm, append = make_step(w)
+    step, attn, norm, append, prep = make_step(w)
     if args.attn_only:
         for _ in range(args.warmup):
             attn()
@@ -432,10 +443,11 @@ def main():
     for _ in range(args.warmup):
         step()
     # Timed region: K steps bracketed by synchronisations; HIP events on the
-    # launching stream split every step into its three parts, so each kernel's
-    # average duration is measured inside the same region as the step time.
+    # launching stream split every step into its two parts (q/k norm + RoPE +
+    # V append, attention), so the attention kernel's average duration is
+    # measured inside the same region as the step time.
     st = torch.cuda.current_stream()
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     e_start, e_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -443,20 +455,23 @@ def main():
     for i in range(args.steps):
         e = ev[i]
         e[0].record(st)
-        norm()
+        prep()
         e[1].record(st)
-        append()
-        e[2].record(st)
         attn()
-        e[3].record(st)
+        e[2].record(st)
     e_end.record(st)
     e_end.synchronize()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = e_start.elapsed_time(e_end) / args.steps
-    ms_norm = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
-    ms_app = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
-    ms_attn = sum(e[2].elapsed_time(e[3]) for e in ev) / args.steps
+    ms_prep = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
+    ms_attn = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
+    # the two HBM kernels on their own (after the timed region), for their rates
+    for _ in range(10):
+        norm()
+        append()
+    ms_norm = time_region(norm, 50)
+    ms_app = time_region(append, 50)
     kvb = 1 if args.kv == "fp8" else 2
     fl = attn_flops()
     ach = fl / (ms_attn * 1e-3) / 1e12
@@ -491,6 +506,9 @@ def main():
                       "frac_hbm": norm_rope_bytes() / (ms_norm * 1e-3) / 1e9 / PEAK_HBM_GBPS},
         "kv_append": {"ms": ms_app, "GB/s": append_bytes() / (ms_app * 1e-3) / 1e9,
                       "frac_hbm": append_bytes() / (ms_app * 1e-3) / 1e9 / PEAK_HBM_GBPS},
+        "step_prep": {"ms": ms_prep, "GB/s": (norm_rope_bytes() + append_bytes()) / (ms_prep * 1e-3) / 1e9,
+                      "what": "fused q/k norm + RoPE + V append (one launch)" if args.kv == "bf16"
+                      else "q/k norm + RoPE, then the fp8 pair append"},
         "wall_s_timed_region": wall,
     }
     if not args.no_stream:

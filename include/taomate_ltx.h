@@ -100,6 +100,30 @@ int ltx_qk_rmsnorm_rope(int dtype, int64_t B, int64_t H, int64_t D,
                         int tab_dtype, void* stream);
 
 /*
+ * ltx_qk_rmsnorm_rope and the key-major bf16 append of the chunk's V in one
+ * launch: the q/k rows as above (dtype LTX_BF16, D 64 or 128) and
+ * v_src [B, v_len, H, D] bf16 (strides v_bs, v_ls, v_hs; D contiguous; rows
+ * 16-byte aligned) transposed into v_dst, element (b, t, h, d) at
+ * v_dst + b*vd_bs + h*vd_hs + d*vd_ds + t (the arena's V layout, as
+ * ltx_kv_append with d_ls == 1).  Replaces, in one pass over HBM, the q/k
+ * norm + RoPE (kv_cache.py:1406-1417) and the V half of the cache append
+ * (_cat_cache, kv_cache.py:394-398) of attention_with_cache.
+ */
+int ltx_qk_rmsnorm_rope_v(int dtype, int64_t B, int64_t H, int64_t D,
+                          const void* q_in, int64_t q_len, int64_t q_in_bs, int64_t q_in_ls,
+                          void* q_out, int64_t q_out_bs, int64_t q_out_ls,
+                          const void* gamma_q, float eps_q,
+                          const void* q_cos, const void* q_sin, int64_t q_tb, int64_t q_th,
+                          int64_t q_tt,
+                          const void* k_in, int64_t k_len, int64_t k_in_bs, int64_t k_in_ls,
+                          void* k_out, int64_t k_out_bs, int64_t k_out_ls,
+                          const void* gamma_k, float eps_k,
+                          const void* k_cos, const void* k_sin, int64_t k_tb, int64_t k_th,
+                          int64_t k_tt, int tab_dtype,
+                          const void* v_src, int64_t v_len, int64_t v_bs, int64_t v_ls, int64_t v_hs,
+                          void* v_dst, int64_t vd_bs, int64_t vd_hs, int64_t vd_ds, void* stream);
+
+/*
  * KV append into a preallocated arena (copy, transpose or fp8 quantise).
  * Replaces _cat_cache / torch.cat (ltx_causal/transformer/kv_cache.py:394-398,
  * block cache update :2642-2656): the new tokens are written once into their

@@ -35,6 +35,12 @@ SIGNATURES = {
                             _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _f32, _ptr, _ptr, _i64,
                             _i64, _i64,
                             _int, _ptr],
+    "ltx_qk_rmsnorm_rope_v": [_int, _i64, _i64, _i64,
+                              _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _f32, _ptr, _ptr, _i64,
+                              _i64, _i64,
+                              _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _f32, _ptr, _ptr, _i64,
+                              _i64, _i64, _int,
+                              _ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr],
     "ltx_kv_append": [_int, _int, _i64, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64,
                       _i64, _i64, _ptr, _i64, _i64, _i64, _ptr],
     "ltx_kv_append_fp8_pair": [_i64, _i64, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _i64,

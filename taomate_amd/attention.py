@@ -87,9 +87,12 @@ def _check_bf16(*ts):
 
 
 def _norm_rope(attn: CausalLTXAttention, q_lin: torch.Tensor, k_lin: torch.Tensor, pe, k_pe,
-               k_out: Optional[torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor]:
+               k_out: Optional[torch.Tensor], v_in: Optional[torch.Tensor] = None,
+               v_out: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """q = rope(q_norm(q_lin)), k = rope(k_norm(k_lin)) in one launch
-    (kv_cache.py:1406-1417).  ``k_out`` may be an arena slot view [B, L, H, D]."""
+    (kv_cache.py:1406-1417).  ``k_out`` may be an arena slot view [B, L, H, D];
+    with ``v_in`` / ``v_out`` (the arena's key-major V slots) the V append
+    rides in the same launch."""
     _check_bf16(q_lin, k_lin)
     H, D = attn.heads, attn.dim_head
     q = torch.empty_like(q_lin)
@@ -100,7 +103,7 @@ def _norm_rope(attn: CausalLTXAttention, q_lin: torch.Tensor, k_lin: torch.Tenso
     _check_bf16(gq, gk)
     eq = attn.q_norm.eps if attn.q_norm.eps is not None else torch.finfo(q_lin.dtype).eps
     ek = attn.k_norm.eps if attn.k_norm.eps is not None else torch.finfo(k_lin.dtype).eps
-    kernels.qk_rmsnorm_rope(q_lin, q, gq, eq, pe, H, D, k_lin, k, gk, ek, kp)
+    kernels.qk_rmsnorm_rope(q_lin, q, gq, eq, pe, H, D, k_lin, k, gk, ek, kp, v_in=v_in, v_out=v_out)
     return q, k
 
 
@@ -268,8 +271,8 @@ def attention_with_cache(
     if arena is not None and not arena.fp8:
         slot = arena.alloc(real)
         k_dst = arena.slots("k", slot, real)
-        q, _ = _norm_rope(attn, q_lin, k_lin, pe, k_pe, k_dst)
-        kernels.kv_append(v_lin.view(B, real, H, D), arena.slots("v", slot, real))
+        q, _ = _norm_rope(attn, q_lin, k_lin, pe, k_pe, k_dst, v_lin.view(B, real, H, D),
+                          arena.slots("v", slot, real))
         new_k = KVSpanView(arena, "k", [(slot, real)])
         new_v = KVSpanView(arena, "v", [(slot, real)])
         segs.append(KVSegment(k_dst, arena.slots("v", slot, real)))

@@ -10,6 +10,7 @@
 #include <type_traits>
 
 #include "ltx_common.h"
+#include "kv_transpose.h"
 
 namespace ltx {
 
@@ -242,54 +243,14 @@ inline int launch_quant_pair(const QuantPair& a, int ntensors, int64_t L, int64_
   return LTX_OK;
 }
 
-// Key-major append: a 64-token x D tile of one (b, h) goes through LDS so both
-// the token-major reads and the key-major writes are 16-byte vector accesses.
+// Key-major append: one block per 64-token tile of one (b, h) (kv_transpose.h).
 template <typename TS, int D>
 __global__ void __launch_bounds__(256) kv_transpose_kernel(
     const TS* __restrict__ src, int64_t s_bs, int64_t s_ls, int64_t s_hs, uint16_t* __restrict__ dst,
     int64_t d_bs, int64_t d_hs, int64_t d_ds, int64_t L) {
-  constexpr int TT = 64;        // tokens per tile
-  constexpr int RS = D + 2;     // LDS row stride (elements): column reads spread over banks
-  __shared__ uint16_t tile[TT * RS];
-  const int64_t l0 = (int64_t)blockIdx.x * TT;
-  const int h = blockIdx.y, b = blockIdx.z;
-  const int rows = (int)((L - l0) < TT ? (L - l0) : TT);
-  constexpr int CPR = D / 8;
-  for (int idx = threadIdx.x; idx < TT * CPR; idx += blockDim.x) {
-    const int r = idx / CPR, c = idx % CPR;
-    if (r >= rows) continue;
-    const TS* sp = src + b * s_bs + (l0 + r) * s_ls + h * s_hs + c * 8;
-    uint32_t w[4];
-    if constexpr (sizeof(TS) == 2) {
-      const uint4 v = *reinterpret_cast<const uint4*>(sp);
-      w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
-    } else {
-      const float4 a = reinterpret_cast<const float4*>(sp)[0];
-      const float4 bb = reinterpret_cast<const float4*>(sp)[1];
-      w[0] = pack_bf16x2(a.x, a.y); w[1] = pack_bf16x2(a.z, a.w);
-      w[2] = pack_bf16x2(bb.x, bb.y); w[3] = pack_bf16x2(bb.z, bb.w);
-    }
-    uint32_t* tp = reinterpret_cast<uint32_t*>(&tile[r * RS + c * 8]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) tp[i] = w[i];
-  }
-  __syncthreads();
-  // write: thread -> (d, 8-token chunk)
-  for (int idx = threadIdx.x; idx < D * (TT / 8); idx += blockDim.x) {
-    const int d = idx / (TT / 8), ch = idx % (TT / 8);
-    const int t0 = ch * 8;
-    if (t0 >= rows) continue;
-    uint16_t* dp = dst + b * d_bs + h * d_hs + d * d_ds + l0 + t0;
-    if (t0 + 8 <= rows) {
-      uint32_t w[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        w[i] = (uint32_t)tile[(t0 + 2 * i) * RS + d] | ((uint32_t)tile[(t0 + 2 * i + 1) * RS + d] << 16);
-      *reinterpret_cast<uint4*>(dp) = make_uint4(w[0], w[1], w[2], w[3]);
-    } else {
-      for (int i = 0; t0 + i < rows; ++i) dp[i] = tile[(t0 + i) * RS + d];
-    }
-  }
+  __shared__ uint16_t tile[transpose_lds_elems<D>()];
+  kv_transpose_tile<TS, D>(src, s_bs, s_ls, s_hs, dst, d_bs, d_hs, d_ds, L, blockIdx.x, blockIdx.y, blockIdx.z,
+                           tile);
 }
 
 struct SpanTable {
@@ -333,6 +294,7 @@ extern "C" int ltx_kv_append(int src_dtype, int dst_dtype, int64_t B, int64_t L,
               "ltx_kv_append: dst_dtype must be BF16 or F8E4M3");
   LTX_REQUIRE(B >= 1 && B <= 65535 && L >= 0 && H >= 1 && H <= 65535 && D >= 8 && D % 8 == 0,
               "ltx_kv_append: bad shape");
+  if (L == 0) return LTX_OK;  // nothing to append (an empty tensor may have no storage)
   LTX_REQUIRE(src && dst, "ltx_kv_append: null pointer");
   const int64_t ssz = src_dtype == LTX_BF16 ? 2 : 4;
   const int64_t dsz = dst_dtype == LTX_BF16 ? 2 : 1;

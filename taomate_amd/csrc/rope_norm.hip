@@ -5,6 +5,7 @@
 // workgroup, and writes the normalised, rotated row once.
 
 #include "ltx_common.h"
+#include "kv_transpose.h"
 
 namespace ltx {
 
@@ -259,8 +260,7 @@ struct NormWork {
   int64_t rg;
   int b, side;
 };
-__device__ __forceinline__ NormWork norm_work(int ncombo, int B) {
-  const int64_t bid = blockIdx.x;
+__device__ __forceinline__ NormWork norm_work(int64_t bid, int ncombo, int B) {
   const int64_t x = bid & 7, t = bid >> 3;
   NormWork w;
   const int combo = (int)(t % ncombo);
@@ -270,11 +270,13 @@ __device__ __forceinline__ NormWork norm_work(int ncombo, int B) {
   return w;
 }
 
+// The rows of work item ``bid`` (see norm_work); every thread of the block
+// calls it (one barrier when normalising).
 template <typename T, typename TT>
-__global__ void __launch_bounds__(256) qk_norm_rope_kernel(NormRopeSide qs, NormRopeSide ks,
-                                                           int H, int D, int B, int nsides) {
+__device__ __forceinline__ void norm_rope_rows(const NormRopeSide& qs, const NormRopeSide& ks, int H, int D, int B,
+                                               int nsides, int64_t bid) {
   constexpr int R = NR_ROWS;
-  const NormWork wk = norm_work(B * nsides, B);
+  const NormWork wk = norm_work(bid, B * nsides, B);
   const NormRopeSide& sd = (wk.side == 0) ? qs : ks;
   const int64_t row0 = wk.rg * R;
   if (row0 >= sd.len) return;  // uniform across the block
@@ -400,6 +402,40 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(NormRopeSide qs, Norm
   }
 }
 
+template <typename T, typename TT>
+__global__ void __launch_bounds__(256) qk_norm_rope_kernel(NormRopeSide qs, NormRopeSide ks,
+                                                           int H, int D, int B, int nsides) {
+  norm_rope_rows<T, TT>(qs, ks, H, D, B, nsides, blockIdx.x);
+}
+
+// V [B, L, H, DV] bf16 rows into a key-major bf16 store, 64-token tiles.
+struct VKeyAppend {
+  const uint16_t* src;
+  int64_t s_bs, s_ls, s_hs;
+  uint16_t* dst;
+  int64_t d_bs, d_hs, d_ds, L;
+  int H;
+};
+
+// One launch for the q/k norm + RoPE rows (blocks [0, n_norm)) and the
+// key-major append of the chunk's V (the blocks after, one per (token tile,
+// head, batch)): both stream HBM, and the V tiles fill the CUs while the
+// norm rows drain instead of waiting for a second launch.
+template <typename TT, int DV>
+__global__ void __launch_bounds__(256) qk_norm_rope_v_kernel(NormRopeSide qs, NormRopeSide ks, int H, int D,
+                                                             int B, int nsides, int64_t n_norm, VKeyAppend va) {
+  __shared__ uint16_t tile[transpose_lds_elems<DV>()];
+  if ((int64_t)blockIdx.x < n_norm) {  // uniform across the block
+    norm_rope_rows<uint16_t, TT>(qs, ks, H, D, B, nsides, blockIdx.x);
+    return;
+  }
+  const int64_t t = (int64_t)blockIdx.x - n_norm;
+  const int64_t ntx = (va.L + kTransposeTokens - 1) / kTransposeTokens;
+  const int64_t hb = t / ntx;
+  kv_transpose_tile<uint16_t, DV>(va.src, va.s_bs, va.s_ls, va.s_hs, va.dst, va.d_bs, va.d_hs, va.d_ds, va.L,
+                                  t % ntx, (int)(hb % va.H), (int)(hb / va.H), tile);
+}
+
 }  // namespace ltx
 
 using namespace ltx;
@@ -458,19 +494,28 @@ extern "C" int ltx_rope_table(void* cos_out, void* sin_out, int out_dtype, const
   return LTX_OK;
 }
 
-extern "C" int ltx_qk_rmsnorm_rope(int dtype, int64_t B, int64_t H, int64_t D,
-                                   const void* q_in, int64_t q_len, int64_t q_in_bs, int64_t q_in_ls,
-                                   void* q_out, int64_t q_out_bs, int64_t q_out_ls,
-                                   const void* gamma_q, float eps_q,
-                                   const void* q_cos, const void* q_sin, int64_t q_tb, int64_t q_th,
-                                   int64_t q_tt,
-                                   const void* k_in, int64_t k_len, int64_t k_in_bs, int64_t k_in_ls,
-                                   void* k_out, int64_t k_out_bs, int64_t k_out_ls,
-                                   const void* gamma_k, float eps_k,
-                                   const void* k_cos, const void* k_sin, int64_t k_tb, int64_t k_th,
-                                   int64_t k_tt,
-                                   int tab_dtype, void* stream) {
-  clear_error();
+namespace {
+
+// Validated launch of the norm rows: the per-side arguments, block size and
+// grid (nblocks = 0: no rows).
+struct NormLaunch {
+  NormRopeSide qs, ks;
+  int threads, nsides;
+  int64_t nblocks;
+};
+
+int norm_setup(int dtype, int64_t B, int64_t H, int64_t D,
+                      const void* q_in, int64_t q_len, int64_t q_in_bs, int64_t q_in_ls,
+                      void* q_out, int64_t q_out_bs, int64_t q_out_ls,
+                      const void* gamma_q, float eps_q,
+                      const void* q_cos, const void* q_sin, int64_t q_tb, int64_t q_th,
+                      int64_t q_tt,
+                      const void* k_in, int64_t k_len, int64_t k_in_bs, int64_t k_in_ls,
+                      void* k_out, int64_t k_out_bs, int64_t k_out_ls,
+                      const void* gamma_k, float eps_k,
+                      const void* k_cos, const void* k_sin, int64_t k_tb, int64_t k_th,
+                      int64_t k_tt,
+                      int tab_dtype, NormLaunch* nl) {
   LTX_REQUIRE(dtype == LTX_F32 || dtype == LTX_BF16, "ltx_qk_rmsnorm_rope: dtype must be F32 or BF16");
   LTX_REQUIRE(tab_dtype == LTX_F32 || tab_dtype == LTX_BF16,
               "ltx_qk_rmsnorm_rope: tab_dtype must be F32 or BF16");
@@ -512,29 +557,115 @@ extern "C" int ltx_qk_rmsnorm_rope(int dtype, int64_t B, int64_t H, int64_t D,
   NormRopeSide ks{k_in, k_out, gamma_k, k_cos, k_sin, k_in ? k_len : 0, k_in_bs, k_in_ls, k_out_bs,
                   k_out_ls, k_tb, k_th, k_tt, eps_k};
   const int64_t rows = k_in ? (q_len > k_len ? q_len : k_len) : q_len;
-  if (rows == 0) return LTX_OK;
+  if (rows == 0) {
+    nl->nblocks = 0;
+    return LTX_OK;
+  }
   LTX_REQUIRE(rows <= 0x7FFFFFFF, "ltx_qk_rmsnorm_rope: too many rows");
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int nsides = k_in ? 2 : 1;
   const int64_t groups = ceil_div(rows, NR_ROWS);
   const int64_t nblocks = ceil_div(groups, 8) * 8 * B * nsides;
   LTX_REQUIRE(nblocks <= 0x7FFFFFFF, "ltx_qk_rmsnorm_rope: grid too large");
-  const dim3 grid((unsigned)nblocks);
+  nl->qs = qs;
+  nl->ks = ks;
+  nl->threads = (int)threads;
+  nl->nsides = nsides;
+  nl->nblocks = nblocks;
+  return LTX_OK;
+}
+
+}  // namespace
+
+extern "C" int ltx_qk_rmsnorm_rope(int dtype, int64_t B, int64_t H, int64_t D,
+                                   const void* q_in, int64_t q_len, int64_t q_in_bs, int64_t q_in_ls,
+                                   void* q_out, int64_t q_out_bs, int64_t q_out_ls,
+                                   const void* gamma_q, float eps_q,
+                                   const void* q_cos, const void* q_sin, int64_t q_tb, int64_t q_th,
+                                   int64_t q_tt,
+                                   const void* k_in, int64_t k_len, int64_t k_in_bs, int64_t k_in_ls,
+                                   void* k_out, int64_t k_out_bs, int64_t k_out_ls,
+                                   const void* gamma_k, float eps_k,
+                                   const void* k_cos, const void* k_sin, int64_t k_tb, int64_t k_th,
+                                   int64_t k_tt,
+                                   int tab_dtype, void* stream) {
+  clear_error();
+  NormLaunch nl;
+  const int rc = norm_setup(dtype, B, H, D, q_in, q_len, q_in_bs, q_in_ls, q_out, q_out_bs, q_out_ls, gamma_q, eps_q, q_cos, q_sin,
+                       q_tb, q_th, q_tt, k_in, k_len, k_in_bs, k_in_ls, k_out, k_out_bs, k_out_ls, gamma_k, eps_k,
+                       k_cos, k_sin, k_tb, k_th, k_tt, tab_dtype, &nl);
+  if (rc != LTX_OK || nl.nblocks == 0) return rc;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)nl.nblocks), block((unsigned)nl.threads);
+  const NormRopeSide &qs = nl.qs, &ks = nl.ks;
+  const int nsides = nl.nsides;
   if (dtype == LTX_BF16) {
     if (tab_dtype == LTX_BF16)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<uint16_t, uint16_t>), grid, dim3((unsigned)threads), 0,
-                         st, qs, ks, (int)H, (int)D, (int)B, nsides);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<uint16_t, uint16_t>), grid, block, 0, st, qs, ks, (int)H, (int)D,
+                         (int)B, nsides);
     else
-      hipLaunchKernelGGL((qk_norm_rope_kernel<uint16_t, float>), grid, dim3((unsigned)threads), 0, st,
-                         qs, ks, (int)H, (int)D, (int)B, nsides);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<uint16_t, float>), grid, block, 0, st, qs, ks, (int)H, (int)D,
+                         (int)B, nsides);
   } else {
     if (tab_dtype == LTX_BF16)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<float, uint16_t>), grid, dim3((unsigned)threads), 0, st,
-                         qs, ks, (int)H, (int)D, (int)B, nsides);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<float, uint16_t>), grid, block, 0, st, qs, ks, (int)H, (int)D,
+                         (int)B, nsides);
     else
-      hipLaunchKernelGGL((qk_norm_rope_kernel<float, float>), grid, dim3((unsigned)threads), 0, st, qs,
-                         ks, (int)H, (int)D, (int)B, nsides);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<float, float>), grid, block, 0, st, qs, ks, (int)H, (int)D,
+                         (int)B, nsides);
   }
   LTX_LAUNCH_CHECK("ltx_qk_rmsnorm_rope");
+  return LTX_OK;
+}
+
+extern "C" int ltx_qk_rmsnorm_rope_v(int dtype, int64_t B, int64_t H, int64_t D,
+                                     const void* q_in, int64_t q_len, int64_t q_in_bs, int64_t q_in_ls,
+                                     void* q_out, int64_t q_out_bs, int64_t q_out_ls,
+                                     const void* gamma_q, float eps_q,
+                                     const void* q_cos, const void* q_sin, int64_t q_tb, int64_t q_th,
+                                     int64_t q_tt,
+                                     const void* k_in, int64_t k_len, int64_t k_in_bs, int64_t k_in_ls,
+                                     void* k_out, int64_t k_out_bs, int64_t k_out_ls,
+                                     const void* gamma_k, float eps_k,
+                                     const void* k_cos, const void* k_sin, int64_t k_tb, int64_t k_th,
+                                     int64_t k_tt, int tab_dtype,
+                                     const void* v_src, int64_t v_len, int64_t v_bs, int64_t v_ls, int64_t v_hs,
+                                     void* v_dst, int64_t vd_bs, int64_t vd_hs, int64_t vd_ds, void* stream) {
+  clear_error();
+  LTX_REQUIRE(dtype == LTX_BF16, "ltx_qk_rmsnorm_rope_v: bf16 rows only");
+  LTX_REQUIRE(D == 64 || D == 128, "ltx_qk_rmsnorm_rope_v: head dim must be 64 or 128");
+  LTX_REQUIRE(v_len >= 0 && (v_len == 0 || (v_src && v_dst)), "ltx_qk_rmsnorm_rope_v: V pointers");
+  if (v_len > 0) {
+    LTX_REQUIRE(((uintptr_t)v_src % 16) == 0 && (v_bs * 2) % 16 == 0 && (v_ls * 2) % 16 == 0 &&
+                    (v_hs * 2) % 16 == 0,
+                "ltx_qk_rmsnorm_rope_v: V rows must be 16-byte aligned");
+    LTX_REQUIRE(((uintptr_t)v_dst % 16) == 0 && (vd_bs * 2) % 16 == 0 && (vd_hs * 2) % 16 == 0 &&
+                    (vd_ds * 2) % 16 == 0,
+                "ltx_qk_rmsnorm_rope_v: key-major V must start on a 16-byte boundary (8-slot aligned)");
+  }
+  NormLaunch nl;
+  const int rc = norm_setup(dtype, B, H, D, q_in, q_len, q_in_bs, q_in_ls, q_out, q_out_bs, q_out_ls, gamma_q, eps_q, q_cos, q_sin,
+                       q_tb, q_th, q_tt, k_in, k_len, k_in_bs, k_in_ls, k_out, k_out_bs, k_out_ls, gamma_k, eps_k,
+                       k_cos, k_sin, k_tb, k_th, k_tt, tab_dtype, &nl);
+  if (rc != LTX_OK) return rc;
+  const int64_t v_tiles = ceil_div(v_len, kTransposeTokens) * H * B;
+  const int64_t nblocks = nl.nblocks + v_tiles;
+  if (nblocks == 0) return LTX_OK;
+  LTX_REQUIRE(nblocks <= 0x7FFFFFFF, "ltx_qk_rmsnorm_rope_v: grid too large");
+  const VKeyAppend va{(const uint16_t*)v_src, v_bs, v_ls, v_hs, (uint16_t*)v_dst, vd_bs, vd_hs, vd_ds, v_len,
+                      (int)H};
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // the V tiles run with the norm's block size (a multiple of 64 threads up to
+  // 256, or 16 / 32): kv_transpose_tile strides by blockDim
+  const dim3 grid((unsigned)nblocks), block((unsigned)(nl.nblocks > 0 ? nl.threads : 256));
+#define LTX_NRV(TT, DV)                                                                                  \
+  hipLaunchKernelGGL((qk_norm_rope_v_kernel<TT, DV>), grid, block, 0, st, nl.qs, nl.ks, (int)H, (int)D, \
+                     (int)B, nl.nsides, nl.nblocks, va)
+  if (tab_dtype == LTX_BF16) {
+    if (D == 128) LTX_NRV(uint16_t, 128); else LTX_NRV(uint16_t, 64);
+  } else {
+    if (D == 128) LTX_NRV(float, 128); else LTX_NRV(float, 64);
+  }
+#undef LTX_NRV
+  LTX_LAUNCH_CHECK("ltx_qk_rmsnorm_rope_v");
   return LTX_OK;
 }

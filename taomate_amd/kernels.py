@@ -89,9 +89,12 @@ def qk_rmsnorm_rope(q_in: torch.Tensor, q_out: torch.Tensor, gamma_q: Optional[t
                     eps_q: Optional[float], q_tab, H: int, D: int,
                     k_in: Optional[torch.Tensor] = None, k_out: Optional[torch.Tensor] = None,
                     gamma_k: Optional[torch.Tensor] = None, eps_k: Optional[float] = None,
-                    k_tab=None) -> None:
-    """ltx_qk_rmsnorm_rope.  eps None skips the norm; a None table skips RoPE."""
-    _need_gpu(q_in, q_out, k_in, k_out, gamma_q, gamma_k)
+                    k_tab=None, v_in: Optional[torch.Tensor] = None, v_out: Optional[torch.Tensor] = None) -> None:
+    """ltx_qk_rmsnorm_rope.  eps None skips the norm; a None table skips RoPE.
+    With ``v_in`` [B, L, H, D] and a key-major bf16 ``v_out`` view of the same
+    shape (the arena's V slots), the V append rides in the same launch
+    (ltx_qk_rmsnorm_rope_v)."""
+    _need_gpu(q_in, q_out, k_in, k_out, gamma_q, gamma_k, v_in, v_out)
     HD = H * D
     B = q_in.shape[0]
     dt = q_in.dtype
@@ -121,14 +124,26 @@ def qk_rmsnorm_rope(q_in: torch.Tensor, q_out: torch.Tensor, gamma_q: Optional[t
     for g in (gamma_q, gamma_k):
         if g is not None and (g.numel() != HD or not g.is_contiguous()):
             raise ValueError("gamma must be a contiguous [H*D] vector")
-    N.call("ltx_qk_rmsnorm_rope", _code(q_in), B, H, D,
-           q_in.data_ptr(), ql, qbs, qls, q_out.data_ptr(), qobs, qols,
-           _ptr(gamma_q), -1.0 if eps_q is None else float(eps_q),
-           _ptr(qc), _ptr(qs), qtb, qth, qtt,
-           _ptr(k_in), kl, kbs, kls, _ptr(k_out), kobs, kols,
-           _ptr(gamma_k), -1.0 if eps_k is None else float(eps_k),
-           _ptr(kc), _ptr(ks), ktb, kth, ktt,
-           tab_code, _stream(q_in))
+    args = (_code(q_in), B, H, D,
+            q_in.data_ptr(), ql, qbs, qls, q_out.data_ptr(), qobs, qols,
+            _ptr(gamma_q), -1.0 if eps_q is None else float(eps_q),
+            _ptr(qc), _ptr(qs), qtb, qth, qtt,
+            _ptr(k_in), kl, kbs, kls, _ptr(k_out), kobs, kols,
+            _ptr(gamma_k), -1.0 if eps_k is None else float(eps_k),
+            _ptr(kc), _ptr(ks), ktb, kth, ktt, tab_code)
+    if v_in is None and v_out is None:
+        N.call("ltx_qk_rmsnorm_rope", *args, _stream(q_in))
+        return
+    if v_in is None or v_out is None:
+        raise ValueError("v_in and v_out go together")
+    if v_in.dim() != 4 or v_out.shape != v_in.shape or v_in.shape[0] != B or v_in.shape[2:] != (H, D):
+        raise ValueError(f"V {tuple(v_in.shape)} -> {tuple(v_out.shape)} does not match B={B} H={H} D={D}")
+    if v_in.dtype != torch.bfloat16 or v_out.dtype != torch.bfloat16 or v_in.stride(3) != 1:
+        raise ValueError("V must be bf16 with a contiguous head dim")
+    if v_out.stride(1) != 1:
+        raise ValueError("v_out must be key-major (token stride 1)")
+    N.call("ltx_qk_rmsnorm_rope_v", *args, v_in.data_ptr(), v_in.shape[1], v_in.stride(0), v_in.stride(1),
+           v_in.stride(2), v_out.data_ptr(), v_out.stride(0), v_out.stride(2), v_out.stride(3), _stream(q_in))
 
 
 def kv_append(src: torch.Tensor, dst: torch.Tensor, scales: Optional[torch.Tensor] = None,

@@ -66,8 +66,7 @@ def prefill_kv(attn: CausalLTXAttention, x: torch.Tensor, pe, arena: KVArena) ->
         kernels.kv_append_fp8_pair(k.view(B, L, H, D), kd, arena.scale_slots("k", slot, L), v_lin.view(B, L, H, D),
                                    vd, arena.scale_slots("v", slot, L), arena.frame_tokens)
     else:
-        kernels.qk_rmsnorm_rope(k_lin, kd, gk, ek, pe, H, D)
-        kernels.kv_append(v_lin.view(B, L, H, D), vd)
+        kernels.qk_rmsnorm_rope(k_lin, kd, gk, ek, pe, H, D, v_in=v_lin.view(B, L, H, D), v_out=vd)
     return KVSpanView(arena, "k", [(slot, L)]), KVSpanView(arena, "v", [(slot, L)])
 
 

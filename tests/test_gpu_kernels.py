@@ -125,6 +125,41 @@ def test_qk_rmsnorm_rope_shared_table_path(dev, B, L, H, D):
     assert torch.equal(qa, qb) and torch.equal(ka, kb)
 
 
+@pytest.mark.parametrize("B,L,H,D,Lv", [(2, 1152, 32, 128, 1152), (1, 192, 8, 64, 192), (2, 37, 16, 64, 37),
+                                         (1, 64, 8, 128, 0), (2, 5, 32, 128, 200)])
+def test_qk_rmsnorm_rope_v_fused_equals_separate(dev, B, L, H, D, Lv):
+    """The fused launch (q/k norm + RoPE rows and the key-major V tiles in one
+    grid) writes exactly what the two separate kernels write, including the
+    V store's untouched slots; V lengths that are not a multiple of the 64-token
+    tile, no V at all, and more V tokens than q/k rows."""
+    g = gen(21)
+    HD = H * D
+    q = randn((B, L, HD), g, torch.bfloat16, 3.0).to(dev)
+    k = randn((B, L, HD), g, torch.bfloat16, 0.5).to(dev)
+    v = randn((B, Lv, H, D), g, torch.bfloat16).to(dev)
+    gq = (1 + 0.1 * randn((HD,), g)).to(torch.bfloat16).to(dev)
+    gk = (1 + 0.1 * randn((HD,), g)).to(torch.bfloat16).to(dev)
+    cos, sin = OR.causal_precompute_freqs_cis((1, L, 1), HD, start_frame=3, num_attention_heads=H,
+                                              batch=1, dtype=torch.bfloat16)
+    tab = (cos.to(dev), sin.to(dev))
+    slots = -(-(Lv + 72) // 8) * 8
+    outs = []
+    for fused in (False, True):
+        qo, ko = torch.empty_like(q), torch.empty_like(k)
+        store = torch.zeros(B, H, D, slots, dtype=torch.bfloat16, device=dev)
+        vview = store.permute(0, 3, 1, 2)[:, 64:64 + Lv]
+        if fused:
+            kernels.qk_rmsnorm_rope(q, qo, gq, 1e-6, tab, H, D, k, ko, gk, 1e-6, tab, v_in=v, v_out=vview)
+        else:
+            kernels.qk_rmsnorm_rope(q, qo, gq, 1e-6, tab, H, D, k, ko, gk, 1e-6, tab)
+            kernels.kv_append(v, vview)
+        outs.append((qo, ko, store))
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    assert torch.equal(outs[1][2].permute(0, 3, 1, 2)[:, 64:64 + Lv], v)
+
+
 def test_norm_only_and_rope_only(dev):
     g = gen(5)
     B, L, H, D = 1, 64, 4, 64

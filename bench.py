@@ -55,8 +55,13 @@ def norm_rope_bytes() -> float:
     return 2 * (2 * B * LQ * HD * 2) + 2 * HD * 2 + 2 * (H * LQ * (D // 2) * 2)
 
 
-def append_bytes() -> float:
-    return 2 * B * LQ * HD * 2  # V read + written
+def append_bytes(kv_dtype: str = "bf16") -> float:
+    """bf16 arena: V read and written key-major.  fp8 arena: the bf16 K and V
+    rows read, their e4m3 codes and one float32 scale per (batch, head, frame)
+    of each written."""
+    if kv_dtype == "fp8":
+        return 2 * B * LQ * HD * 2 + 2 * B * LQ * HD + 2 * B * H * (LQ // FRAME) * 4
+    return 2 * B * LQ * HD * 2
 
 
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "attention_b2_h32_d128_1152q_4608k_hbm_traffic.md")
@@ -322,18 +327,31 @@ def dit_bench(dev, steps: int = 5, warmup: int = 2, learned_memory: bool = False
 
 
 def time_region(fn, iters: int) -> float:
-    """Average ms per call over `iters` back-to-back calls, HIP events on the
-    launching stream (the attention-only profiling mode and the standalone
+    """Average device ms per call over `iters` back-to-back calls, HIP events on
+    the launching stream (the attention-only profiling mode and the standalone
     rates of the norm and append kernels; the step figures come from the timed
-    step loop)."""
+    step loop).  The calls are queued behind a bounded device spin so that the
+    host's launch cost stays out of the interval: the start event must still
+    be pending once the last call is queued, else the spin is lengthened and
+    the measurement repeated (a short kernel launched from Python otherwise
+    times the host, not the kernel)."""
     st = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record(st)
-    for _ in range(iters):
-        fn()
-    e1.record(st)
-    e1.synchronize()
+    cycles = 1 << 20
+    for attempt in range(6):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        torch.cuda._sleep(cycles)
+        e0.record(st)
+        for _ in range(iters):
+            fn()
+        ahead = not e0.query()
+        e1.record(st)
+        e1.synchronize()
+        if ahead:
+            return e0.elapsed_time(e1) / iters
+        cycles *= 4
+    print("time_region: the host could not queue ahead of the device; the figure includes launch cost",
+          file=sys.stderr)
     return e0.elapsed_time(e1) / iters
 
 
@@ -459,6 +477,7 @@ def main():
         e[1].record(st)
         attn()
         e[2].record(st)
+    t_enq = time.perf_counter() - t0   # host time to queue the K steps
     e_end.record(st)
     e_end.synchronize()
     torch.cuda.synchronize()
@@ -504,12 +523,16 @@ def main():
         "attention_query_tokens_per_s": B * LQ / (ms_attn * 1e-3),
         "norm_rope": {"ms": ms_norm, "GB/s": norm_rope_bytes() / (ms_norm * 1e-3) / 1e9,
                       "frac_hbm": norm_rope_bytes() / (ms_norm * 1e-3) / 1e9 / PEAK_HBM_GBPS},
-        "kv_append": {"ms": ms_app, "GB/s": append_bytes() / (ms_app * 1e-3) / 1e9,
-                      "frac_hbm": append_bytes() / (ms_app * 1e-3) / 1e9 / PEAK_HBM_GBPS},
-        "step_prep": {"ms": ms_prep, "GB/s": (norm_rope_bytes() + append_bytes()) / (ms_prep * 1e-3) / 1e9,
+        "kv_append": {"ms": ms_app, "GB/s": append_bytes(args.kv) / (ms_app * 1e-3) / 1e9,
+                      "frac_hbm": append_bytes(args.kv) / (ms_app * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+                      "what": "V transposed into the key-major arena" if args.kv == "bf16"
+                      else "K and V quantised to e4m3 into the arena (one launch)"},
+        "step_prep": {"ms": ms_prep,
+                      "GB/s": (norm_rope_bytes() + append_bytes(args.kv)) / (ms_prep * 1e-3) / 1e9,
                       "what": "fused q/k norm + RoPE + V append (one launch)" if args.kv == "bf16"
                       else "q/k norm + RoPE, then the fp8 pair append"},
         "wall_s_timed_region": wall,
+        "host_enqueue_ms_per_step": t_enq * 1e3 / args.steps,
     }
     if not args.no_stream:
         res["long_stream"] = stream_bench(dev)

@@ -342,7 +342,26 @@ ATTN_CASES = [
     (1, 75, 32, 64, [1152]),                      # V2A
     (2, 130, 4, 128, [1, 63, 65, 7]),             # ragged tails, tiny segments
     (1, 1, 2, 128, [5]),                          # single query / few keys
+    # the 16-segment maximum (after the two empty ones are dropped), ragged
+    (1, 64, 4, 128, [8, 0, 17, 64, 1, 130, 9, 33, 0, 64, 2, 71, 5, 40, 16, 3, 7, 11]),
+    (1, 128, 8, 128, [40000, 128]),               # long key range: 627 key tiles
 ]
+
+
+def test_flash_attn_segment_limits(dev):
+    """More than 16 non-empty segments, or none with keys, is refused before
+    any launch."""
+    q = torch.zeros(1, 8, 2, 64, dtype=torch.bfloat16, device=dev)
+    out = torch.empty_like(q)
+    ka = torch.zeros(1, 17 * 8, 2, 64, dtype=torch.bfloat16, device=dev)
+    segs = [KVSegment(ka[:, 8 * i:8 * i + 8], ka[:, 8 * i:8 * i + 8]) for i in range(17)]
+    with pytest.raises(ValueError, match="segments"):
+        kernels.flash_attn(q, segs, out)
+    with pytest.raises(ValueError, match="no keys"):
+        kernels.flash_attn(q, [KVSegment(ka[:, :0], ka[:, :0])], out)
+    kernels.flash_attn(q, segs[:16], out)   # the maximum itself runs
+    torch.cuda.synchronize()
+    assert torch.equal(out, torch.zeros_like(out))   # V = 0
 
 
 @pytest.mark.parametrize("vlayout", ["token", "key"])

@@ -168,7 +168,7 @@ def make_step(w):
     return step, attn, norm, append, prep
 
 
-def stream_bench(dev, n_chunks: int = 60, kv_dtype: str = "fp8", warm_chunks: int = 60):
+def stream_bench(dev, n_chunks: int = 60, kv_dtype: str = "fp8", warm_chunks: int = 60, fuse_qkv: bool = True):
     """Sustained rate of the long stream: one video self-attention layer at the
     512x768 chunk shape (B=2, 32 heads x 128, d=4096, weights ~N(0, 0.02^2),
     inputs ~N(0, 1), seed 4) run through ``n_chunks`` 3-frame chunks with the
@@ -189,6 +189,8 @@ def stream_bench(dev, n_chunks: int = 60, kv_dtype: str = "fp8", warm_chunks: in
         for lin in (attn.to_q, attn.to_k, attn.to_v, attn.to_out[0]):
             lin.weight.copy_(torch.randn(lin.weight.shape, generator=g, device=dev) * 0.02)
             lin.bias.zero_()
+    if fuse_qkv:
+        attn.fuse_qkv_()
     # eight distinct chunk inputs, used in turn
     xs = [torch.randn(B, LQ, HD, generator=g, device=dev).to(torch.bfloat16) for _ in range(8)]
     xa = torch.randn(B, FRAME, HD, generator=g, device=dev).to(torch.bfloat16)
@@ -211,12 +213,13 @@ def stream_bench(dev, n_chunks: int = 60, kv_dtype: str = "fp8", warm_chunks: in
     return {"query_tokens_per_s": n_chunks * B * LQ / secs, "unit": "query-tokens/s",
             "ms_per_chunk": secs / n_chunks * 1e3, "chunks": n_chunks, "kv_dtype": kv_dtype,
             "memory_refreshes": st.memory_version, "cached_keys_after_last_chunk": keys,
+            "qkv_projection": "one packed GEMM" if fuse_qkv else "three GEMMs",
             "workload": "one 32x128 video self-attention layer (d=4096, B=2) over 60 chunks of 3 frames at "
                         "16x24: anchor 1 frame pinned | memory 2 frames refreshed every 4 chunks | 12-frame "
                         "window | current chunk, whole layer per chunk (projections included)"}
 
 
-def dit_bench(dev, steps: int = 5, warmup: int = 2, learned_memory: bool = False):
+def dit_bench(dev, steps: int = 5, warmup: int = 2, learned_memory: bool = False, fuse_qkv: bool = True):
     """One denoising step of the 48-block dual-stream model (video 32 x 128,
     d = 4096; audio 32 x 64, d = 2048; 4x GELU FFNs; AdaLN modulation) for one
     512x768 chunk at B = 2: 1152 video tokens over the 3456 cached keys of the
@@ -236,6 +239,8 @@ def dit_bench(dev, steps: int = 5, warmup: int = 2, learned_memory: bool = False
 
     cfg = Dm.AVConfig(learned_memory_enabled=learned_memory, learned_memory_color_film_enabled=learned_memory)
     model = Dm.build_model(cfg, dev, seed=3)
+    if fuse_qkv:
+        model.fuse_qkv_()
     n_params = sum(p.numel() for p in model.parameters())
     g = torch.Generator(device=dev)
     g.manual_seed(3)
@@ -317,6 +322,7 @@ def dit_bench(dev, steps: int = 5, warmup: int = 2, learned_memory: bool = False
     res = {"ms_per_step": ms, "chunk_query_tokens_per_s": B * LQ / (ms * 1e-3), "params": n_params,
            "attention_ms": ms_attn, "attention_share": ms_attn / ms_inst, "attention_calls": len(attn_events),
            "outputs_finite": finite, "learned_memory": learned_memory,
+           "qkv_projection": "one packed GEMM per self-attention" if fuse_qkv else "three GEMMs",
            "workload": "48 dual-stream blocks (video 32x128 d=4096, audio 32x64 d=2048, 4x GELU FFNs, AdaLN), "
                        "one denoising step of a 512x768 chunk at B=2: 1152 video queries over 3456 cached + 1152 "
                        "keys, 75 audio over 600 + 75, 1024 text keys (20% masked), A2V 1152x75, V2A 75x1152"
@@ -411,6 +417,8 @@ def main():
     ap.add_argument("--stream-only", action="store_true", help="run only the 60-chunk long-stream measurement")
     ap.add_argument("--no-dit", action="store_true", help="skip the 48-block denoising-step measurement")
     ap.add_argument("--dit-only", action="store_true", help="run only the 48-block denoising-step measurement")
+    ap.add_argument("--no-fuse-qkv", action="store_true",
+                    help="stream and 48-block step: three q/k/v GEMMs instead of one packed GEMM per self-attention")
     ap.add_argument("--dit-learned-memory", action="store_true",
                     help="the 48-block step with learned-memory adapters on every 4th block")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -433,10 +441,10 @@ def main():
         print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "launches": 3}))
         return
     if args.stream_only:
-        print(json.dumps(stream_bench(dev)))
+        print(json.dumps(stream_bench(dev, fuse_qkv=not args.no_fuse_qkv)))
         return
     if args.dit_only:
-        print(json.dumps(dit_bench(dev, learned_memory=args.dit_learned_memory)))
+        print(json.dumps(dit_bench(dev, learned_memory=args.dit_learned_memory, fuse_qkv=not args.no_fuse_qkv)))
         return
     if args.copy_bandwidth:
         for mib in (64, 256, 1024, 4096):
@@ -535,9 +543,9 @@ def main():
         "host_enqueue_ms_per_step": t_enq * 1e3 / args.steps,
     }
     if not args.no_stream:
-        res["long_stream"] = stream_bench(dev)
+        res["long_stream"] = stream_bench(dev, fuse_qkv=not args.no_fuse_qkv)
     if not args.no_dit:
-        res["dit_step"] = dit_bench(dev, learned_memory=args.dit_learned_memory)
+        res["dit_step"] = dit_bench(dev, learned_memory=args.dit_learned_memory, fuse_qkv=not args.no_fuse_qkv)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(res))

@@ -49,6 +49,41 @@ class CausalLTXAttention(nn.Module):
         self.to_gate_logits = nn.Linear(query_dim, heads, bias=True) if apply_gated_attention else None
         self.to_out = nn.Sequential(nn.Linear(self.inner_dim, query_dim, bias=True), nn.Identity())
 
+    def fuse_qkv_(self) -> "CausalLTXAttention":
+        """Re-home to_q / to_k / to_v's weights and biases in one packed
+        [3·inner, dim] buffer, the three parameters becoming row views of it
+        (no extra memory; names, values and state_dict unchanged), so that a
+        self-attention projects q, k and v with one GEMM.  A no-op for
+        cross-attention (K and V come from the context).  Anything that
+        re-creates a parameter afterwards (``load_state_dict(assign=True)``,
+        ``.to()``, assignment) ends the packing and the three GEMMs run again."""
+        if self.is_cross_attention:
+            return self
+        lins = (self.to_q, self.to_k, self.to_v)
+        with torch.no_grad():
+            w = torch.cat([lin.weight.detach() for lin in lins], 0)
+            b = torch.cat([lin.bias.detach() for lin in lins], 0)
+        n = self.inner_dim
+        for i, lin in enumerate(lins):
+            lin.weight = nn.Parameter(w[i * n:(i + 1) * n], requires_grad=lin.weight.requires_grad)
+            lin.bias = nn.Parameter(b[i * n:(i + 1) * n], requires_grad=lin.bias.requires_grad)
+        self._qkv_packed = (w, b)
+        return self
+
+    def _packed_qkv(self) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
+        """The packed (weight, bias) while the three projections still alias it."""
+        pk = getattr(self, "_qkv_packed", None)
+        if pk is None:
+            return None
+        w, b = pk
+        n = self.inner_dim
+        for i, lin in enumerate((self.to_q, self.to_k, self.to_v)):
+            if lin.weight.data_ptr() != w[i * n].data_ptr() or lin.bias is None or \
+                    lin.bias.data_ptr() != b[i * n:].data_ptr() or lin.weight.shape != w[i * n:(i + 1) * n].shape:
+                self._qkv_packed = None   # a parameter was replaced: drop the stale buffer
+                return None
+        return w, b
+
     def _apply_rope(self, x: torch.Tensor, freqs_cis: Tuple[torch.Tensor, torch.Tensor]) -> torch.Tensor:
         """causal_attention.py:326-338 (SPLIT only)."""
         if self.rope_type != CausalRopeType.SPLIT:
@@ -84,6 +119,19 @@ def _check_bf16(*ts):
     for t in ts:
         if t is not None and t.dtype != torch.bfloat16:
             raise TypeError(f"the gfx950 attention path runs bf16 activations, got {t.dtype}")
+
+
+def _project_qkv(attn: CausalLTXAttention, x: torch.Tensor, ctx: torch.Tensor):
+    """to_q(x), to_k(ctx), to_v(ctx) (kv_cache.py:1406-1408).  A self-attention
+    packed by ``fuse_qkv_`` runs one GEMM and returns three column views of its
+    [B, L, 3·inner] output (row stride 3·inner), which the norm / RoPE and
+    append kernels read in place."""
+    packed = attn._packed_qkv() if ctx is x else None
+    if packed is None:
+        return attn.to_q(x), attn.to_k(ctx), attn.to_v(ctx)
+    y = torch.nn.functional.linear(x, *packed)
+    n = attn.inner_dim
+    return y[..., :n], y[..., n:2 * n], y[..., 2 * n:]
 
 
 def _norm_rope(attn: CausalLTXAttention, q_lin: torch.Tensor, k_lin: torch.Tensor, pe, k_pe,
@@ -259,7 +307,7 @@ def attention_with_cache(
     B, L, _ = x.shape
     ctx = x if context is None else context
     H, D = attn.heads, attn.dim_head
-    q_lin, k_lin, v_lin = attn.to_q(x), attn.to_k(ctx), attn.to_v(ctx)
+    q_lin, k_lin, v_lin = _project_qkv(attn, x, ctx)
     _check_bf16(q_lin, k_lin, v_lin)
     Lk_new = k_lin.shape[1]
     real = Lk_new if new_kv_real_len is None else min(int(new_kv_real_len), Lk_new)

@@ -111,7 +111,9 @@ def load_generator(model_ckpt_path: str, device="cuda", dtype: torch.dtype = tor
 def save_generator(model: AVModel, path: str) -> None:
     """Write ``{"generator_ema": {"model.<name>": tensor}}`` (the layout
     load_model_generator reads), atomically."""
-    sd = {_PREFIX + k: v.detach().cpu().contiguous() for k, v in model.state_dict().items()}
+    # own copies: parameters may be views of one buffer (fuse_qkv_), which
+    # safetensors refuses and torch.save would write whole
+    sd = {_PREFIX + k: v.detach().to("cpu", copy=True).contiguous() for k, v in model.state_dict().items()}
     os.makedirs(os.path.dirname(os.path.abspath(path)) or ".", exist_ok=True)
     tmp = f"{path}.tmp.{os.getpid()}"
     if path.endswith(".safetensors"):

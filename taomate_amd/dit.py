@@ -394,6 +394,15 @@ class AVModel(nn.Module):
         self.audio_norm_out = nn.LayerNorm(ad, elementwise_affine=False, eps=1e-6)
         self.audio_proj_out = nn.Linear(ad, cfg.out_channels)
 
+    def fuse_qkv_(self) -> "AVModel":
+        """Pack the q/k/v projections of every self-attention (video and audio)
+        into one GEMM each; parameter names, values and memory are unchanged
+        (CausalLTXAttention.fuse_qkv_)."""
+        for m in self.modules():
+            if isinstance(m, CausalLTXAttention):
+                m.fuse_qkv_()
+        return self
+
     def _timestep(self, sigma: torch.Tensor, adaln: AdaLayerNormSingle, batch: int, dtype):
         """causal_model.py:426-455."""
         ts, emb = adaln((sigma * self.cfg.timestep_scale_multiplier).flatten(), dtype)

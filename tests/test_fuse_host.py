@@ -1,0 +1,82 @@
+"""Packed q/k/v projections (CausalLTXAttention.fuse_qkv_) on the CPU: the
+packing keeps every parameter's name and value, the one GEMM equals the three
+(kv_cache.py:1406-1408), and anything that replaces a parameter ends the
+packing instead of leaving the GEMM on stale weights."""
+import os
+
+import torch
+
+import taomate_amd as T
+from taomate_amd import dit as D
+from taomate_amd.attention import _project_qkv
+from taomate_amd.checkpoint import load_generator, save_generator
+
+
+def _module(seed=0, **kw):
+    torch.manual_seed(seed)
+    m = T.CausalLTXAttention(64, heads=2, dim_head=32, **kw)
+    with torch.no_grad():
+        for lin in (m.to_q, m.to_k, m.to_v):
+            lin.bias.normal_()
+    return m
+
+
+def test_packing_keeps_values_and_matches_three_gemms():
+    m = _module()
+    before = {k: v.clone() for k, v in m.state_dict().items()}
+    x = torch.randn(2, 5, 64)
+    want = (m.to_q(x), m.to_k(x), m.to_v(x))
+    m.fuse_qkv_()
+    after = m.state_dict()
+    assert before.keys() == after.keys()
+    for k in before:
+        assert torch.equal(before[k], after[k]), k
+    w, b = m._packed_qkv()
+    assert w.shape == (3 * 64, 64) and b.shape == (3 * 64,)
+    assert m.to_k.weight.data_ptr() == w[64].data_ptr()   # a view, not a copy
+    got = _project_qkv(m, x, x)
+    assert got[0].stride(1) == 3 * 64                      # column views of one [B, L, 3n] output
+    for g_, w_ in zip(got, want):
+        torch.testing.assert_close(g_, w_, rtol=1e-6, atol=1e-6)
+    # in-place updates of a projection reach the packed GEMM
+    with torch.no_grad():
+        m.to_v.weight.mul_(2.0)
+    torch.testing.assert_close(_project_qkv(m, x, x)[2], m.to_v(x), rtol=1e-6, atol=1e-6)
+
+
+def test_replacing_a_parameter_ends_the_packing():
+    m = _module().fuse_qkv_()
+    sd = {k: v.clone() * 3 for k, v in m.state_dict().items()}
+    m.load_state_dict(sd, assign=True)
+    assert m._packed_qkv() is None and m._qkv_packed is None
+    x = torch.randn(1, 4, 64)
+    for g_, w_ in zip(_project_qkv(m, x, x), (m.to_q(x), m.to_k(x), m.to_v(x))):
+        assert torch.equal(g_, w_)
+    m2 = _module().fuse_qkv_().to(torch.float64)
+    assert m2._packed_qkv() is None
+
+
+def test_cross_attention_and_foreign_context_stay_unpacked():
+    m = T.CausalLTXAttention(64, context_dim=32, heads=2, dim_head=32).fuse_qkv_()
+    assert getattr(m, "_qkv_packed", None) is None
+    s = _module().fuse_qkv_()
+    x, ctx = torch.randn(1, 3, 64), torch.randn(1, 7, 64)
+    q, k, v = _project_qkv(s, x, ctx)   # K / V from another tensor: three GEMMs
+    assert k.shape[1] == 7 and torch.equal(k, s.to_k(ctx))
+
+
+def test_model_packs_every_self_attention_and_saves(tmp_path):
+    cfg = D.AVConfig(num_layers=2, video_dim=128, audio_dim=64, video_heads=2, audio_heads=1, video_d_head=64,
+                     audio_d_head=64, in_channels=8)
+    model = D.AVModel(cfg)
+    before = {k: v.clone() for k, v in model.state_dict().items()}
+    model.fuse_qkv_()
+    packed = [n for n, m in model.named_modules() if isinstance(m, T.CausalLTXAttention) and m._packed_qkv()]
+    assert sorted(packed) == sorted(f"transformer_blocks.{i}.{a}" for i in range(2) for a in ("attn1", "audio_attn1"))
+    for ext in (".safetensors", ".pt"):
+        path = os.path.join(tmp_path, "g" + ext)
+        save_generator(model, path)
+        back = load_generator(path, device="cpu", dtype=torch.float32)
+        sd = back.state_dict()
+        for k, v in before.items():
+            assert torch.equal(sd[k], v), k

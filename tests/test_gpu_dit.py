@@ -58,8 +58,11 @@ def _pes(dev=None):
             vcross, pe((LA,), cross, CFG.audio_heads, A0, True))
 
 
-def test_block_stack_matches_oracle(dev):
+@pytest.mark.parametrize("packed", [False, True], ids=["qkv3", "qkv_packed"])
+def test_block_stack_matches_oracle(dev, packed):
     model = D.build_model(CFG, dev, seed=3)
+    if packed:
+        model.fuse_qkv_()   # video and audio self-attentions: one q/k/v GEMM each
     params = {n: p.detach().float().cpu() for n, p in model.named_parameters()}
     x = _inputs()
     ref_v, ref_a = OD.forward_chunk(params, CFG, x["video"], x["audio"], x["sigma"], x["vctx"], x["actx"],

@@ -81,14 +81,20 @@ def _layer_reference(B, gh, gw, H, Dh, seed, w):
     return _ORACLE[key]
 
 
+@pytest.mark.parametrize("packed", [False, True], ids=["qkv3", "qkv_packed"])
 @pytest.mark.parametrize("case", LAYERS, ids=[c[0] for c in LAYERS])
-def test_attention_with_cache_layer(dev, case):
+def test_attention_with_cache_layer(dev, case, packed):
+    """packed: the q/k/v projections run as one GEMM (fuse_qkv_), whose three
+    column views (row stride 3·H·D) feed the norm / RoPE and append kernels."""
     name, B, gh, gw, H, Dh, seed, kvd = case
     d = H * Dh
     hw = gh * gw
     segs = SEGS_SMALL if H == 8 else SEGS_FULL
     cur_f0, cur_nf = (10, 2) if H == 8 else (12, 3)
     attn, w = make_layer(dev, d, H, Dh, seed)
+    if packed:
+        attn.fuse_qkv_()
+        assert attn._packed_qkv() is not None
     xs, xc, ref, ref_k = _layer_reference(B, gh, gw, H, Dh, seed, w)
     # GPU: same calls through an arena cache
     total = sum(nf for _, _, nf in segs) * hw + cur_nf * hw

@@ -54,7 +54,13 @@ def prefill_kv(attn: CausalLTXAttention, x: torch.Tensor, pe, arena: KVArena) ->
     a segment, with no attention output."""
     B, L, _ = x.shape
     H, D = attn.heads, attn.dim_head
-    k_lin, v_lin = attn.to_k(x), attn.to_v(x)
+    packed = attn._packed_qkv()
+    if packed is None:
+        k_lin, v_lin = attn.to_k(x), attn.to_v(x)
+    else:   # the K and V rows of a packed q/k/v weight (fuse_qkv_): one GEMM
+        n = attn.inner_dim
+        kv = torch.nn.functional.linear(x, packed[0][n:], packed[1][n:])
+        k_lin, v_lin = kv[..., :n], kv[..., n:]
     _check_bf16(k_lin, v_lin)
     gk = attn.k_norm.weight
     ek = attn.k_norm.eps if attn.k_norm.eps is not None else torch.finfo(k_lin.dtype).eps

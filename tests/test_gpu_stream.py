@@ -32,6 +32,8 @@ def _inputs_and_reference(w, grid):
 @pytest.mark.parametrize("kv_dtype,grid", [("bf16", (8, 12)), ("fp8", (8, 16))], ids=["bf16_8x12", "fp8_8x16"])
 def test_chunk_stream_60_chunks(dev, kv_dtype, grid):
     attn, w = make_layer(dev, H * DH, H, DH, 50)
+    if kv_dtype == "fp8":
+        attn.fuse_qkv_()   # packed q/k/v GEMM, memory re-prefill included (bf16 keeps three GEMMs)
     xa, xm, chunks, (ref_outs, ref_k, ref_v, ref_segs) = _inputs_and_reference(w, grid)
     st = ChunkStream(attn, grid, B, dev, kv_dtype=kv_dtype)
     worst = 1.0

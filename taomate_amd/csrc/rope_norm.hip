@@ -249,8 +249,9 @@ __device__ __forceinline__ float rnd(float v) {
 }
 
 // Rows handled by one workgroup of the fused kernel (all loads of its rows are
-// issued before the first reduction).
-constexpr int NR_ROWS = 1;
+// issued before the first reduction).  Measured at 1152 rows x 4096, B = 2:
+// 2 rows 17.8 us, 1 row 18.5 us, 4 rows 19.8 us.
+constexpr int NR_ROWS = 2;
 
 // Workgroup -> (row group, batch, side).  The combos (batch, side) of one row
 // group share its RoPE-table rows; blocks are dispatched round-robin over the

@@ -319,7 +319,21 @@ def dit_bench(dev, steps: int = 5, warmup: int = 2, learned_memory: bool = False
             kernels.flash_attn = real_flash
         ms_inst = s0.elapsed_time(s1)
         ms_attn = sum(a.elapsed_time(b) for a, b in attn_events)
+        # the same steps with the text cross-attention's K/V kept across steps
+        # (the reference's exact text K/V cache, off by default there and in
+        # the figure above): the first call projects, the timed ones reuse
+        model.cache_text_kv_()
+        step()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        e1.synchronize()
+        ms_tkv = e0.elapsed_time(e1) / steps
+        model.cache_text_kv_(False)
     res = {"ms_per_step": ms, "chunk_query_tokens_per_s": B * LQ / (ms * 1e-3), "params": n_params,
+           "ms_per_step_text_kv_cached": ms_tkv,
            "attention_ms": ms_attn, "attention_share": ms_attn / ms_inst, "attention_calls": len(attn_events),
            "outputs_finite": finite, "learned_memory": learned_memory,
            "qkv_projection": "one packed GEMM per self-attention" if fuse_qkv else "three GEMMs",

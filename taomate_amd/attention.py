@@ -14,6 +14,7 @@ plus the new chunk.  Activations are bf16, as on the reference's GPU path.
 """
 from __future__ import annotations
 
+import collections
 import weakref
 from typing import Dict, List, Optional, Tuple
 
@@ -84,6 +85,35 @@ class CausalLTXAttention(nn.Module):
                 return None
         return w, b
 
+    def cache_text_kv_(self, enabled: bool = True, size: int = 4) -> "CausalLTXAttention":
+        """Keep the normalised K and the V of the last ``size`` contexts
+        (_get_cached_text_cross_kv, kv_cache.py:707-760: the exact,
+        inference-only LRU of the text cross-attention's projections, off by
+        default there too).  A hit needs the same context tensor object,
+        unmodified since (its version counter), and unchanged K/V parameters;
+        anything else projects again."""
+        self._text_kv_cache = collections.OrderedDict() if enabled else None
+        self._text_kv_size = int(size)
+        return self
+
+    def _cached_text_kv(self, ctx: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+        """k = k_norm(to_k(ctx)), v = to_v(ctx), from the cache when it holds them."""
+        params = tuple((p.data_ptr(), p._version) for p in (self.to_k.weight, self.to_k.bias, self.to_v.weight,
+                                                              self.to_v.bias, self.k_norm.weight) if p is not None)
+        key = (id(ctx), ctx.data_ptr(), tuple(ctx.shape), tuple(ctx.stride()), ctx.dtype, str(ctx.device),
+               ctx._version, params)
+        cache = self._text_kv_cache
+        hit = cache.get(key)
+        if hit is not None and hit[0]() is ctx:
+            cache.move_to_end(key)
+            return hit[1], hit[2]
+        k = _norm_one(self.k_norm, self.to_k(ctx), None, self.heads, self.dim_head)
+        v = self.to_v(ctx)
+        cache[key] = (weakref.ref(ctx), k, v)
+        while len(cache) > self._text_kv_size:
+            cache.popitem(last=False)
+        return k, v
+
     def _apply_rope(self, x: torch.Tensor, freqs_cis: Tuple[torch.Tensor, torch.Tensor]) -> torch.Tensor:
         """causal_attention.py:326-338 (SPLIT only)."""
         if self.rope_type != CausalRopeType.SPLIT:
@@ -103,8 +133,13 @@ class CausalLTXAttention(nn.Module):
             raise NotImplementedError("training block masks are not part of the inference path")
         B = x.shape[0]
         ctx = x if context is None else context
-        q_lin, k_lin, v = self.to_q(x), self.to_k(ctx), self.to_v(ctx)
-        q, k = _norm_rope(self, q_lin, k_lin, pe, k_pe, None)
+        if context is not None and pe is None and k_pe is None and getattr(self, "_text_kv_cache", None) is not None \
+                and not torch.is_grad_enabled():
+            k, v = self._cached_text_kv(context)
+            q = _norm_one(self.q_norm, self.to_q(x), None, self.heads, self.dim_head)
+        else:
+            q_lin, k_lin, v = self.to_q(x), self.to_k(ctx), self.to_v(ctx)
+            q, k = _norm_rope(self, q_lin, k_lin, pe, k_pe, None)
         if logit_log_scale is not None:
             q = q * logit_log_scale
         H, D = self.heads, self.dim_head
@@ -153,6 +188,16 @@ def _norm_rope(attn: CausalLTXAttention, q_lin: torch.Tensor, k_lin: torch.Tenso
     ek = attn.k_norm.eps if attn.k_norm.eps is not None else torch.finfo(k_lin.dtype).eps
     kernels.qk_rmsnorm_rope(q_lin, q, gq, eq, pe, H, D, k_lin, k, gk, ek, kp, v_in=v_in, v_out=v_out)
     return q, k
+
+
+def _norm_one(norm: nn.RMSNorm, x_lin: torch.Tensor, pe, H: int, D: int) -> torch.Tensor:
+    """rope(norm(x_lin)) for one side (the same per-row arithmetic as the q/k launch)."""
+    g = norm.weight
+    _check_bf16(x_lin, g)
+    eps = norm.eps if norm.eps is not None else torch.finfo(x_lin.dtype).eps
+    out = torch.empty_like(x_lin)
+    kernels.qk_rmsnorm_rope(x_lin, out, g, eps, pe, H, D)
+    return out
 
 
 def _finish(attn: CausalLTXAttention, out: torch.Tensor, x: torch.Tensor) -> torch.Tensor:

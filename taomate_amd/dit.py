@@ -403,6 +403,15 @@ class AVModel(nn.Module):
                 m.fuse_qkv_()
         return self
 
+    def cache_text_kv_(self, enabled: bool = True, size: int = 4) -> "AVModel":
+        """Keep each block's text cross-attention K/V (video and audio) across
+        calls with the same context tensor (CausalLTXAttention.cache_text_kv_;
+        kv_cache.py:707-760, off by default as there)."""
+        for blk in self.transformer_blocks:
+            blk.attn2.cache_text_kv_(enabled, size)
+            blk.audio_attn2.cache_text_kv_(enabled, size)
+        return self
+
     def _timestep(self, sigma: torch.Tensor, adaln: AdaLayerNormSingle, batch: int, dtype):
         """causal_model.py:426-455."""
         ts, emb = adaln((sigma * self.cfg.timestep_scale_multiplier).flatten(), dtype)

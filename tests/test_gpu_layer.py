@@ -186,6 +186,42 @@ def test_text_cross_attention_with_padding_mask(dev):
     assert cosine(out, ref) >= 0.9999
 
 
+def test_text_kv_cache_is_exact(dev):
+    """cache_text_kv_: calls with the same context tensor reuse its K/V and give
+    bit-identical outputs to projecting again; an in-place change of the
+    context or of a K/V weight, or another context tensor, projects again."""
+    B, H, Dh, d = 2, 8, 64, 512
+    attn, w = make_layer(dev, d, H, Dh, 31, context_dim=d, gate=True)
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(B, 96, d, generator=g).to(dev, torch.bfloat16)
+    ctx = torch.randn(B, 40, d, generator=g).to(dev, torch.bfloat16)
+    keep = torch.ones(B, 40, dtype=torch.int64)
+    keep[1, 30:] = 0
+    m = OA.prepare_attention_mask(keep, torch.bfloat16).to(dev)
+    with torch.no_grad():
+        plain = attn(x, context=ctx, mask=m)
+        attn.cache_text_kv_()
+        first = attn(x, context=ctx, mask=m)
+        again = attn(x, context=ctx, mask=m)
+        assert len(attn._text_kv_cache) == 1
+        assert torch.equal(first, plain) and torch.equal(again, plain)
+        ctx.add_(0.25)                                   # in place: a new version, projected again
+        moved = attn(x, context=ctx, mask=m)
+        attn.cache_text_kv_(False)
+        assert torch.equal(moved, attn(x, context=ctx, mask=m))
+        attn.cache_text_kv_()
+        attn(x, context=ctx, mask=m)
+        attn.to_v.weight.mul_(0.5)                       # a K/V parameter changed in place
+        halved = attn(x, context=ctx, mask=m)
+        attn.cache_text_kv_(False)
+        assert torch.equal(halved, attn(x, context=ctx, mask=m))
+        attn.cache_text_kv_(size=2)
+        for _ in range(3):
+            attn(x, context=ctx.clone(), mask=m)         # distinct tensors: LRU of 2
+        assert len(attn._text_kv_cache) == 2
+    torch.cuda.synchronize()
+
+
 def test_denoise_steps_do_not_commit(dev):
     """Three denoise-step calls on a snapshot, then the commit: the committed cache
     holds only the commit pass's keys, and step outputs equal the oracle's."""

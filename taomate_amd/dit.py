@@ -51,6 +51,13 @@ class GELUApprox(nn.Module):
         self.proj = nn.Linear(dim_in, dim_out)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.is_cuda and x.dtype == torch.bfloat16 and self.proj.bias is not None and not torch.is_grad_enabled():
+            # the GEMM's GELU-bias epilogue: tanh-GELU of the float32
+            # accumulator + bias, rounded to bf16 once, instead of a second
+            # pass over the bf16 [tokens, 4·dim] output
+            y = torch._addmm_activation(self.proj.bias, x.reshape(-1, x.shape[-1]), self.proj.weight.t(),
+                                        use_gelu=True)
+            return y.view(*x.shape[:-1], y.shape[-1])
         return F.gelu(self.proj(x), approximate="tanh")
 
 

@@ -164,3 +164,23 @@ def test_block_stack_with_learned_memory_matches_oracle(dev, mode):
         assert err <= 3e-2 * ref.abs().max().item(), err
     # the memory reached both streams
     assert (vo - vo0).abs().max().item() > 1e-2 and (ao - ao0).abs().max().item() > 1e-2
+
+
+@pytest.mark.parametrize("L", [300, 2304])
+def test_ffn_gelu_epilogue(dev, L):
+    """The first FFN GEMM with its tanh-GELU epilogue (bf16, no grad) against
+    float32 tanh-GELU(x W^T + b), and no further from it than the two-pass
+    bf16 form (linear, then gelu) the reference runs."""
+    torch.manual_seed(5)
+    m = D.GELUApprox(512, 2048).to(dev, torch.bfloat16)
+    x = torch.randn(2, L, 512, device=dev).to(torch.bfloat16)
+    with torch.no_grad():
+        y = m(x)
+        two = torch.nn.functional.gelu(m.proj(x), approximate="tanh")
+    ref = torch.nn.functional.gelu(torch.nn.functional.linear(x.float(), m.proj.weight.float(), m.proj.bias.float()),
+                                   approximate="tanh")
+    assert y.shape == two.shape and y.dtype == torch.bfloat16
+    e_epi = (y.float() - ref).abs()
+    e_two = (two.float() - ref).abs()
+    assert e_epi.max().item() <= 2e-2 and e_epi.mean().item() <= 2e-3
+    assert e_epi.mean().item() <= e_two.mean().item() * 1.05

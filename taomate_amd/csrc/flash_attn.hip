@@ -255,16 +255,23 @@ constexpr int kMaxSplit = 8;  // key ranges a tail q-tile may be cut into
 // Combines the `split` partial results of every tail q-tile, launched after the
 // attention kernel on the same stream: out = sum_i w_i o_i / sum_i w_i with
 // w_i = l_i 2^(m_i - max m) and o_i the range's normalised output.  One thread
-// per (query row, 4 output columns): every piece's (max, sum) and O values
-// are loaded up front, so each thread waits for one round of loads.
+// per (query row, 8 output columns): every piece's (max, sum) and 16-byte O
+// chunk are loaded up front, so each thread waits for one round of loads.
+// The output is written as two 8-byte halves (the entry point guarantees
+// 8-byte aligned output rows); the workspace partials are 16-byte aligned.
+constexpr int kCombineCols = 8;
+template <int D>
+constexpr int combine_wg_per_tile() { return kBM / (256 / (D / kCombineCols)); }
+
 template <int D>
 __global__ void __launch_bounds__(256) flash_combine_kernel(const FlashParams p) {
-  constexpr int C4 = D / 4;             // 4-column groups per row
-  constexpr int ROWS = 256 / C4;        // rows per workgroup
+  constexpr int CG = D / kCombineCols;  // 8-column groups per row
+  constexpr int ROWS = 256 / CG;        // rows per workgroup
   constexpr int WG_PER_TILE = kBM / ROWS;
+  static_assert(WG_PER_TILE == combine_wg_per_tile<D>() && ROWS * WG_PER_TILE == kBM, "combine grid");
   const int tail = blockIdx.x / WG_PER_TILE;
-  const int r = (blockIdx.x % WG_PER_TILE) * ROWS + threadIdx.x / C4;
-  const int c4 = threadIdx.x % C4;
+  const int r = (blockIdx.x % WG_PER_TILE) * ROWS + threadIdx.x / CG;
+  const int cg = threadIdx.x % CG;
   const int qtile = p.n_full + tail;
   const int qt = qtile % p.n_qtiles;
   const int bh = qtile / p.n_qtiles;
@@ -273,12 +280,12 @@ __global__ void __launch_bounds__(256) flash_combine_kernel(const FlashParams p)
   if (q >= p.Lq) return;
   const int64_t first = (int64_t)tail * p.split;
   f32x2_t ml[kMaxSplit];
-  uint2 o[kMaxSplit];
+  uint4 o[kMaxSplit];
 #pragma unroll
   for (int i = 0; i < kMaxSplit; ++i) {
     if (i < p.split) {
       ml[i] = *reinterpret_cast<const f32x2_t*>(p.part_ml + ((first + i) * kBM + r) * 2);
-      o[i] = *reinterpret_cast<const uint2*>(p.part_o + ((first + i) * kBM + r) * D + c4 * 4);
+      o[i] = *reinterpret_cast<const uint4*>(p.part_o + ((first + i) * kBM + r) * D + cg * kCombineCols);
     }
   }
   float mmax = -INFINITY;
@@ -286,24 +293,27 @@ __global__ void __launch_bounds__(256) flash_combine_kernel(const FlashParams p)
   for (int i = 0; i < kMaxSplit; ++i)
     if (i < p.split) mmax = fmaxf(mmax, ml[i][0]);
   float lsum = 0.0f;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float acc[kCombineCols] = {};
 #pragma unroll
   for (int i = 0; i < kMaxSplit; ++i) {
     if (i < p.split) {
       const float wgt = ml[i][0] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml[i][0] - mmax) * ml[i][1];
       lsum += wgt;
-      acc.x += wgt * bf16_bits_to_f32(o[i].x & 0xFFFFu);
-      acc.y += wgt * bf16_bits_to_f32(o[i].x >> 16);
-      acc.z += wgt * bf16_bits_to_f32(o[i].y & 0xFFFFu);
-      acc.w += wgt * bf16_bits_to_f32(o[i].y >> 16);
+      const uint32_t w[4] = {o[i].x, o[i].y, o[i].z, o[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[2 * e] += wgt * bf16_bits_to_f32(w[e] & 0xFFFFu);
+        acc[2 * e + 1] += wgt * bf16_bits_to_f32(w[e] >> 16);
+      }
     }
   }
   const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-  uint2 v;
-  v.x = pack_bf16x2(acc.x * inv, acc.y * inv);
-  v.y = pack_bf16x2(acc.z * inv, acc.w * inv);
-  *reinterpret_cast<uint2*>(p.o + b * p.o_bs + (int64_t)q * p.o_ls + h * p.o_hs + c4 * 4) = v;
-  if (p.lse != nullptr && c4 == 0) p.lse[((int64_t)b * p.H + h) * p.Lq + q] = (mmax + __log2f(lsum)) / kLog2e;
+  uint16_t* dst = p.o + b * p.o_bs + (int64_t)q * p.o_ls + h * p.o_hs + cg * kCombineCols;
+  *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(acc[0] * inv, acc[1] * inv),
+                                              pack_bf16x2(acc[2] * inv, acc[3] * inv));
+  *reinterpret_cast<uint2*>(dst + 4) = make_uint2(pack_bf16x2(acc[4] * inv, acc[5] * inv),
+                                                  pack_bf16x2(acc[6] * inv, acc[7] * inv));
+  if (p.lse != nullptr && cg == 0) p.lse[((int64_t)b * p.H + h) * p.Lq + q] = (mmax + __log2f(lsum)) / kLog2e;
 }
 
 template <int D, bool FP8, bool MASK>
@@ -1097,7 +1107,7 @@ template <int D>
 int launch_combine(const FlashParams& p, hipStream_t st) {
   if (p.split <= 1) return LTX_OK;
   const int64_t tail = (int64_t)p.B * p.H * p.n_qtiles - p.n_full;
-  const int64_t wg_per_tile = kBM / (256 / (D / 4));
+  const int64_t wg_per_tile = combine_wg_per_tile<D>();
   hipLaunchKernelGGL((flash_combine_kernel<D>), dim3((unsigned)(tail * wg_per_tile)), dim3(256), 0, st, p);
   LTX_LAUNCH_CHECK("ltx_flash_attn_fwd (combine)");
   return LTX_OK;

@@ -216,9 +216,22 @@ def test_text_kv_cache_is_exact(dev):
         attn.cache_text_kv_(False)
         assert torch.equal(halved, attn(x, context=ctx, mask=m))
         attn.cache_text_kv_(size=2)
-        for _ in range(3):
-            attn(x, context=ctx.clone(), mask=m)         # distinct tensors: LRU of 2
+        ctxs = [ctx.clone() for _ in range(3)]           # three live tensors: LRU of 2
+        for c in ctxs:
+            attn(x, context=c, mask=m)
         assert len(attn._text_kv_cache) == 2
+        # a freed context whose address and version a new tensor reuses is no
+        # hit: the entry's weak reference no longer points at the caller's tensor
+        del ctxs
+        fresh = ctx.clone().mul_(-1.0)
+        attn.cache_text_kv_(False)
+        want = attn(x, context=fresh, mask=m)
+        attn.cache_text_kv_(size=2)
+        for _ in range(2):
+            tmp = ctx.clone()
+            attn(x, context=tmp, mask=m)
+            del tmp
+        assert torch.equal(attn(x, context=fresh, mask=m), want)
     torch.cuda.synchronize()
 
 

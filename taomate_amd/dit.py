@@ -29,7 +29,7 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass
-from typing import List, Optional, Tuple
+from typing import Dict, List, Optional, Tuple
 
 import torch
 import torch.nn as nn
@@ -293,13 +293,33 @@ def _apply_memory(x: torch.Tensor, n: Optional[torch.Tensor], steps, eps: float,
     return x, n
 
 
+def _all_blocks_ada(blocks, batch: int, v_ts, a_ts, v_ss, v_gate, a_ss, a_gate) -> List[Dict[str, tuple]]:
+    """Every block's modulation values (AVBlock.get_ada_values /
+    get_av_ca_ada_values, causal_block.py:434-481) with one add per table kind
+    over the stacked tables of all blocks instead of eight small adds per
+    block: the same elementwise table + timestep sums."""
+    def stacked(name, ts, rows):
+        tab = torch.stack([getattr(b, name)[rows] for b in blocks]).to(device=ts.device, dtype=ts.dtype)
+        n = tab.shape[1]
+        vals = tab[:, None, None] + ts.reshape(batch, ts.shape[1], n, -1)[None]
+        return [v.unbind(dim=2) for v in vals]
+    v = stacked("scale_shift_table", v_ts, slice(None))
+    a = stacked("audio_scale_shift_table", a_ts, slice(None))
+    a_ss4 = stacked("scale_shift_table_a2v_ca_audio", a_ss, slice(0, 4))
+    a_g = stacked("scale_shift_table_a2v_ca_audio", a_gate, slice(4, 5))
+    v_ss4 = stacked("scale_shift_table_a2v_ca_video", v_ss, slice(0, 4))
+    v_g = stacked("scale_shift_table_a2v_ca_video", v_gate, slice(4, 5))
+    return [{"v": v[i], "a": a[i], "a_ca": (*a_ss4[i], *a_g[i]), "v_ca": (*v_ss4[i], *v_g[i])}
+            for i in range(len(blocks))]
+
+
 def block_forward_with_cache(block: AVBlock, vx: torch.Tensor, ax: torch.Tensor, v_ts: torch.Tensor,
                              a_ts: torch.Tensor, video_pe, audio_pe, video_cross_pe, audio_cross_pe,
                              video_ctx: torch.Tensor, audio_ctx: torch.Tensor, video_mask: Optional[torch.Tensor],
                              audio_mask: Optional[torch.Tensor], v_cross_ss: torch.Tensor, v_cross_gate: torch.Tensor,
                              a_cross_ss: torch.Tensor, a_cross_gate: torch.Tensor, cache: LayerKVCache,
                              video_memory: Optional[torch.Tensor] = None, audio_memory: Optional[torch.Tensor] = None,
-                             color_memory: Optional[torch.Tensor] = None):
+                             color_memory: Optional[torch.Tensor] = None, ada: Optional[Dict[str, tuple]] = None):
     """kv_cache.py:2145-2656 (synchronous branch): video self -> video text ->
     audio self -> audio text -> A2V -> V2A -> video FFN -> audio FFN.
     Returns (vx, ax, cache with the chunk's K/V appended).
@@ -325,7 +345,7 @@ def block_forward_with_cache(block: AVBlock, vx: torch.Tensor, ax: torch.Tensor,
     v_mem = any(m is not None and a is not None for m, a in v_steps)
     a_mem = any(m is not None and a is not None for m, a in a_steps)
     # video self-attention, then its residual fused with the text-cross norm
-    sh, sc, g = block.get_ada_values(block.scale_shift_table, B, v_ts, slice(0, 3))
+    sh, sc, g = ada["v"][0:3] if ada else block.get_ada_values(block.scale_shift_table, B, v_ts, slice(0, 3))
     out, vs_k, vs_v = attention_with_cache(block.attn1, _modulate(vx, sc, sh, eps), None, video_pe, None,
                                            cache.video_self_k, cache.video_self_v)
     vx, vn = _residual(vx, out, g, norm=True, eps=eps)
@@ -333,7 +353,7 @@ def block_forward_with_cache(block: AVBlock, vx: torch.Tensor, ax: torch.Tensor,
         vx, vn = _apply_memory(vx, vn, v_steps, eps, need_norm=True)
     v_text = block.attn2(vn, context=video_ctx, mask=video_mask)   # kv_cache.py:1134-1141
     # audio self-attention and text cross-attention
-    sh, sc, g = block.get_ada_values(block.audio_scale_shift_table, B, a_ts, slice(0, 3))
+    sh, sc, g = ada["a"][0:3] if ada else block.get_ada_values(block.audio_scale_shift_table, B, a_ts, slice(0, 3))
     out, as_k, as_v = attention_with_cache(block.audio_attn1, _modulate(ax, sc, sh, eps), None, audio_pe, None,
                                            cache.audio_self_k, cache.audio_self_v)
     ax, an = _residual(ax, out, g, norm=True, eps=eps)
@@ -346,9 +366,9 @@ def block_forward_with_cache(block: AVBlock, vx: torch.Tensor, ax: torch.Tensor,
         vx, _ = _apply_memory(vx, vn, v_steps, eps, need_norm=False)
         ax, _ = _apply_memory(ax, an, a_steps, eps, need_norm=False)
     # cross-modal: both read the norms taken before either update
-    sc_a_a2v, sh_a_a2v, sc_a_v2a, sh_a_v2a, gate_v2a = block.get_av_ca_ada_values(
+    sc_a_a2v, sh_a_a2v, sc_a_v2a, sh_a_v2a, gate_v2a = ada["a_ca"] if ada else block.get_av_ca_ada_values(
         block.scale_shift_table_a2v_ca_audio, B, a_cross_ss, a_cross_gate)
-    sc_v_a2v, sh_v_a2v, sc_v_v2a, sh_v_v2a, gate_a2v = block.get_av_ca_ada_values(
+    sc_v_a2v, sh_v_a2v, sc_v_v2a, sh_v_v2a, gate_a2v = ada["v_ca"] if ada else block.get_av_ca_ada_values(
         block.scale_shift_table_a2v_ca_video, B, v_cross_ss, v_cross_gate)
     a2v, a2v_k, a2v_v = attention_with_cache(block.audio_to_video_attn, _modulate(vx, sc_v_a2v, sh_v_a2v, eps),
                                              _modulate(ax, sc_a_a2v, sh_a_a2v, eps), video_cross_pe,
@@ -357,10 +377,10 @@ def block_forward_with_cache(block: AVBlock, vx: torch.Tensor, ax: torch.Tensor,
                                              _modulate(vx, sc_v_v2a, sh_v_v2a, eps), audio_cross_pe,
                                              video_cross_pe, cache.v2a_k, cache.v2a_v)
     # cross-modal residuals fused with the feed-forward input norms
-    sh, sc, g = block.get_ada_values(block.scale_shift_table, B, v_ts, slice(3, 6))
+    sh, sc, g = ada["v"][3:6] if ada else block.get_ada_values(block.scale_shift_table, B, v_ts, slice(3, 6))
     vx, vn = _residual(vx, a2v, gate_a2v, norm=True, scale=sc, shift=sh, eps=eps)
     vx, _ = _residual(vx, block.ff(vn), g, eps=eps)
-    sh, sc, g = block.get_ada_values(block.audio_scale_shift_table, B, a_ts, slice(3, 6))
+    sh, sc, g = ada["a"][3:6] if ada else block.get_ada_values(block.audio_scale_shift_table, B, a_ts, slice(3, 6))
     ax, an = _residual(ax, v2a, gate_v2a, norm=True, scale=sc, shift=sh, eps=eps)
     ax, _ = _residual(ax, block.audio_ff(an), g, eps=eps)
     new_cache = LayerKVCache(
@@ -477,10 +497,11 @@ class AVModel(nn.Module):
         a_ss, a_gate = self._cross_timestep(sigma, self.av_ca_audio_scale_shift_adaln_single,
                                             self.av_ca_v2a_gate_adaln_single, B, dt)
         new_caches = []
-        for blk, cache in zip(self.transformer_blocks, caches):
+        ada = _all_blocks_ada(self.transformer_blocks, B, v_ts, a_ts, v_ss, v_gate, a_ss, a_gate)
+        for blk, cache, blk_ada in zip(self.transformer_blocks, caches, ada):
             vx, ax, nc = block_forward_with_cache(blk, vx, ax, v_ts, a_ts, video_pe, audio_pe, video_cross_pe,
                                                   audio_cross_pe, video_ctx, audio_ctx, video_mask, audio_mask,
-                                                  v_ss, v_gate, a_ss, a_gate, cache, vm, am, cm)
+                                                  v_ss, v_gate, a_ss, a_gate, cache, vm, am, cm, ada=blk_ada)
             new_caches.append(nc if commit else cache)
             del nc
         if kv_cache_only:

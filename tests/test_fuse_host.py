@@ -80,3 +80,33 @@ def test_model_packs_every_self_attention_and_saves(tmp_path):
         sd = back.state_dict()
         for k, v in before.items():
             assert torch.equal(sd[k], v), k
+
+
+def test_all_blocks_modulation_equals_per_block():
+    """_all_blocks_ada (one add per table kind over the stacked tables of every
+    block) gives bit for bit the values of each block's get_ada_values /
+    get_av_ca_ada_values (causal_block.py:434-481), in bf16 as the step runs."""
+    cfg = D.AVConfig(num_layers=3, video_dim=128, audio_dim=64, video_heads=2, audio_heads=1, video_d_head=64,
+                     audio_d_head=64, in_channels=8)
+    torch.manual_seed(4)
+    model = D.AVModel(cfg).to(torch.bfloat16)
+    with torch.no_grad():
+        for p in model.parameters():
+            p.normal_()
+    B, T = 2, 3
+    r = lambda *s: torch.randn(*s).to(torch.bfloat16)
+    v_ts, a_ts = r(B, T, 6 * 128), r(B, T, 6 * 64)
+    v_ss, v_gate, a_ss, a_gate = r(B, T, 4 * 128), r(B, T, 128), r(B, T, 4 * 64), r(B, T, 64)
+    ada = D._all_blocks_ada(model.transformer_blocks, B, v_ts, a_ts, v_ss, v_gate, a_ss, a_gate)
+    for blk, got in zip(model.transformer_blocks, ada):
+        want = {"v": blk.get_ada_values(blk.scale_shift_table, B, v_ts, slice(0, 6)),
+                "a": blk.get_ada_values(blk.audio_scale_shift_table, B, a_ts, slice(0, 6)),
+                "a_ca": blk.get_av_ca_ada_values(blk.scale_shift_table_a2v_ca_audio, B, a_ss, a_gate),
+                "v_ca": blk.get_av_ca_ada_values(blk.scale_shift_table_a2v_ca_video, B, v_ss, v_gate)}
+        for k in want:
+            assert len(got[k]) == len(want[k]), k
+            for g_, w_ in zip(got[k], want[k]):
+                assert g_.dtype == w_.dtype and torch.equal(g_, w_), k
+        assert all(torch.equal(g_, w_) for g_, w_ in zip(got["v"][3:6],
+                                                         blk.get_ada_values(blk.scale_shift_table, B, v_ts,
+                                                                            slice(3, 6))))

@@ -307,18 +307,24 @@ def dit_bench(dev, steps: int = 5, warmup: int = 2, learned_memory: bool = False
         e1.synchronize()
         ms = e0.elapsed_time(e1) / steps
         finite = bool(torch.isfinite(vo).all() and torch.isfinite(ao).all())
-        # attention share: one more step with events around every attention call
+        # attention share: three more steps with events around every attention
+        # call; the fastest of them (a host stall only lengthens a step) gives
+        # the step time and its attention calls' summed time
         kernels.flash_attn = timed_flash
+        best = None
         try:
-            s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s0.record()
-            step()
-            s1.record()
-            s1.synchronize()
+            for _ in range(3):
+                attn_events.clear()
+                s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s0.record()
+                step()
+                s1.record()
+                s1.synchronize()
+                cur = (s0.elapsed_time(s1), sum(a.elapsed_time(b) for a, b in attn_events), len(attn_events))
+                best = cur if best is None or cur[0] < best[0] else best
         finally:
             kernels.flash_attn = real_flash
-        ms_inst = s0.elapsed_time(s1)
-        ms_attn = sum(a.elapsed_time(b) for a, b in attn_events)
+        ms_inst, ms_attn, n_attn = best
         # the same steps with the text cross-attention's K/V kept across steps
         # (the reference's exact text K/V cache, off by default there and in
         # the figure above): the first call projects, the timed ones reuse
@@ -334,7 +340,7 @@ def dit_bench(dev, steps: int = 5, warmup: int = 2, learned_memory: bool = False
         model.cache_text_kv_(False)
     res = {"ms_per_step": ms, "chunk_query_tokens_per_s": B * LQ / (ms * 1e-3), "params": n_params,
            "ms_per_step_text_kv_cached": ms_tkv,
-           "attention_ms": ms_attn, "attention_share": ms_attn / ms_inst, "attention_calls": len(attn_events),
+           "attention_ms": ms_attn, "attention_share": ms_attn / ms_inst, "attention_calls": n_attn,
            "outputs_finite": finite, "learned_memory": learned_memory,
            "qkv_projection": "one packed GEMM per self-attention" if fuse_qkv else "three GEMMs",
            "workload": "48 dual-stream blocks (video 32x128 d=4096, audio 32x64 d=2048, 4x GELU FFNs, AdaLN), "

@@ -430,6 +430,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--kv", choices=["bf16", "fp8"], default="bf16")
+    ap.add_argument("--settle-seconds", type=float, default=2.0,
+                    help="seconds of back-to-back steps before the warm-up (reported in the 'settle' field)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--attn-only", action="store_true", help="loop only the attention kernel (profiling)")
@@ -486,6 +488,19 @@ def main():
         ms = time_region(attn, args.steps)
         print(json.dumps({"attn_only_ms": ms, "tflops": attn_flops() / ms / 1e9}))
         return
+    # Settle phase (reported as its own field, outside warmup and steps): the
+    # step runs back to back for --settle-seconds of wall time so that the
+    # card leaves its idle clock state before the warm-up and timed steps; a
+    # cold card runs its first milliseconds of work at a lower clock.
+    settle_steps = 0
+    torch.cuda.synchronize()
+    t_settle = time.perf_counter()
+    while time.perf_counter() - t_settle < args.settle_seconds:
+        for _ in range(20):
+            step()
+        settle_steps += 20
+        torch.cuda.synchronize()
+    settle_s = time.perf_counter() - t_settle
     for _ in range(args.warmup):
         step()
     # Timed region: K steps bracketed by synchronisations; HIP events on the
@@ -511,8 +526,14 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = e_start.elapsed_time(e_end) / args.steps
-    ms_prep = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
-    ms_attn = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
+    prep_ms = [e[0].elapsed_time(e[1]) for e in ev]
+    attn_ms = [e[1].elapsed_time(e[2]) for e in ev]
+    step_ms = [e[0].elapsed_time(e[2]) for e in ev]
+    ms_prep = sum(prep_ms) / args.steps
+    ms_attn = sum(attn_ms) / args.steps
+
+    def dist(xs):
+        return {"min": min(xs), "median": statistics.median(xs), "max": max(xs)}
     # the two HBM kernels on their own (after the timed region), for their rates
     for _ in range(10):
         norm()
@@ -559,6 +580,9 @@ def main():
                       "GB/s": (norm_rope_bytes() + append_bytes(args.kv)) / (ms_prep * 1e-3) / 1e9,
                       "what": "fused q/k norm + RoPE + V append (one launch)" if args.kv == "bf16"
                       else "q/k norm + RoPE, then the fp8 pair append"},
+        "per_step_ms": {"step": dist(step_ms), "attention": dist(attn_ms), "prep": dist(prep_ms)},
+        "settle": {"seconds": settle_s, "steps": settle_steps,
+                   "what": "back-to-back steps before the warm-up, so the card leaves its idle clock state"},
         "wall_s_timed_region": wall,
         "host_enqueue_ms_per_step": t_enq * 1e3 / args.steps,
     }

@@ -30,6 +30,8 @@
 // fp8 KV: tiles are decoded to bf16 on their way into LDS; the per-(head,
 // frame) scales are folded into the logit scale (K) and into P (V).
 
+#include <mutex>
+
 #include "ltx_common.h"
 
 namespace ltx {
@@ -1142,23 +1144,27 @@ int launch_flash(const FlashParams& p, hipStream_t st) {
 using namespace ltx;
 
 // Resident workgroups the device holds for this kernel (CUs x occupancy),
-// cached per device; one cache per kernel (each instantiation of the
-// template has its own).
+// computed once per device under a once-flag (calls from several host
+// threads may race to fill it); one table per kernel (each instantiation of
+// the template has its own).
+constexpr int kMaxDevices = 64;
 template <auto Kernel>
 int resident_slots(int threads = 256) {
-  static int cache[64][2];  // [device] -> {valid, slots}
+  static std::once_flag once[kMaxDevices];
+  static int slots[kMaxDevices];
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (!cache[dev][0]) {
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  std::call_once(once[dev], [&]() {
     int cus = 0, occ = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, Kernel, threads, 0) != hipSuccess) return 0;
-    cache[dev][1] = cus * (occ > 0 ? occ : 1);
-    cache[dev][0] = 1;
-  }
-  return cache[dev][1];
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, Kernel, threads, 0) != hipSuccess) {
+      slots[dev] = 0;  // no split is planned on this device
+      return;
+    }
+    slots[dev] = cus * (occ > 0 ? occ : 1);
+  });
+  return slots[dev];
 }
-
 
 // Tail q-tiles (those past the last whole round of resident slots) and how
 // many key ranges each is cut into: enough pieces to fill the resident slots

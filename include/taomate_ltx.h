@@ -224,6 +224,31 @@ int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t H, int64_t 
                        int64_t workspace_bytes, void* stream);
 
 /*
+ * ltx_flash_attn_fwd without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ *   Same arguments, semantics and results as ltx_flash_attn_fwd with a
+ *   sufficient workspace; the split partials go to a fixed device array of
+ *   LTX_NOALLOC_SCRATCH_BYTES inside the library (one per device, kept until
+ *   the process ends).  Allocates nothing: no hipMalloc / hipFree, no
+ *   allocating library call.  A call whose split would need more scratch
+ *   than that returns LTX_EINVAL with a message (at most 512 resident
+ *   workgroups x 128 rows x (8 + 2 D) bytes are ever planned on MI355X:
+ *   17.3 MB for D = 128).  Calls that overlap in time on one device share the
+ *   array and race: serialise them (one stream, or events).
+ */
+#define LTX_NOALLOC_SCRATCH_BYTES (24ll << 20)
+int ltx_flash_attn_fwd_noalloc(const void* q, int64_t B, int64_t Lq, int64_t H, int64_t D,
+                               int64_t q_bs, int64_t q_ls, int64_t q_hs, int64_t n_segments,
+                               const void* const* k_ptrs, const void* const* v_ptrs,
+                               const int64_t* seg_lens, int64_t k_bs, int64_t k_ls, int64_t k_hs,
+                               int64_t v_bs, int64_t v_ls, int64_t v_hs, int64_t v_ds, int kv_dtype,
+                               const float* const* k_scales, const float* const* v_scales,
+                               int64_t sc_bs, int64_t sc_hs, int64_t frame_tokens,
+                               const float* key_mask, int64_t mask_bs, void* out, int64_t o_bs,
+                               int64_t o_ls, int64_t o_hs, float* lse, float scale, void* stream);
+
+/*
  * Workspace bytes ltx_flash_attn_fwd can use for a [B, Lq, H, D] query on the
  * current device (0: no split is ever planned for this shape).
  * No counterpart in the reference (its SDPA call has no workspace).

@@ -16,6 +16,7 @@ LIB_NAME = "libtaomate_ltx.so"
 
 F32, BF16, F8E4M3 = 0, 1, 2
 MAX_SEGMENTS = 16
+NOALLOC_SCRATCH_BYTES = 24 << 20  # LTX_NOALLOC_SCRATCH_BYTES
 ABI_VERSION = 1
 
 _i64 = ctypes.c_int64
@@ -50,6 +51,9 @@ SIGNATURES = {
     "ltx_flash_attn_fwd": [_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr,
                            _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _ptr, _ptr, _i64, _i64,
                            _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _ptr, _f32, _ptr, _i64, _ptr],
+    "ltx_flash_attn_fwd_noalloc": [_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr,
+                                   _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _ptr, _ptr, _i64, _i64,
+                                   _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _ptr, _f32, _ptr],
     "ltx_flash_attn_workspace_size": [_i64, _i64, _i64, _i64, _ptr],
     "ltx_adaln": [_i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64,
                   _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _f32, _ptr],

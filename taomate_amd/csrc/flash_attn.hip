@@ -1225,17 +1225,20 @@ extern "C" int ltx_flash_attn_workspace_size(int64_t B, int64_t Lq, int64_t H, i
   return LTX_OK;
 }
 
-extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t H, int64_t D,
-                                  int64_t q_bs, int64_t q_ls, int64_t q_hs, int64_t n_segments,
-                                  const void* const* k_ptrs, const void* const* v_ptrs,
-                                  const int64_t* seg_lens, int64_t k_bs, int64_t k_ls, int64_t k_hs,
-                                  int64_t v_bs, int64_t v_ls, int64_t v_hs, int64_t v_ds, int kv_dtype,
-                                  const float* const* k_scales, const float* const* v_scales,
-                                  int64_t sc_bs, int64_t sc_hs, int64_t frame_tokens,
-                                  const float* key_mask, int64_t mask_bs, void* out, int64_t o_bs,
-                                  int64_t o_ls, int64_t o_hs, float* lse, float scale,
-                                  void* workspace, int64_t workspace_bytes, void* stream) {
-  clear_error();
+// The body of both attention entry points.  `strict_ws`: a planned split
+// whose partials do not fit the workspace is an error (the no-allocation
+// entry point, whose workspace is the fixed scratch array) instead of a
+// fallback to whole q-tiles.
+static int flash_attn_fwd_impl(const void* q, int64_t B, int64_t Lq, int64_t H, int64_t D,
+                               int64_t q_bs, int64_t q_ls, int64_t q_hs, int64_t n_segments,
+                               const void* const* k_ptrs, const void* const* v_ptrs,
+                               const int64_t* seg_lens, int64_t k_bs, int64_t k_ls, int64_t k_hs,
+                               int64_t v_bs, int64_t v_ls, int64_t v_hs, int64_t v_ds, int kv_dtype,
+                               const float* const* k_scales, const float* const* v_scales,
+                               int64_t sc_bs, int64_t sc_hs, int64_t frame_tokens,
+                               const float* key_mask, int64_t mask_bs, void* out, int64_t o_bs,
+                               int64_t o_ls, int64_t o_hs, float* lse, float scale,
+                               void* workspace, int64_t workspace_bytes, bool strict_ws, void* stream) {
   LTX_REQUIRE(q && out, "ltx_flash_attn_fwd: null q/out");
   LTX_REQUIRE(D == 64 || D == 128, "ltx_flash_attn_fwd: head dim %lld unsupported (64 or 128)",
               (long long)D);
@@ -1326,6 +1329,10 @@ extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t 
       const int slots = flash_slots(D, vkey, fp8, key_mask != nullptr);
       plan_split(nq, p.tile_start[n], slots, &n_full, &split);
       if (split > 1 && workspace_bytes_for(nq - n_full, split, D) > workspace_bytes) {
+        LTX_REQUIRE(!strict_ws,
+                    "ltx_flash_attn_fwd_noalloc: this call's split partials need %lld bytes, more than the "
+                    "%lld-byte scratch array",
+                    (long long)workspace_bytes_for(nq - n_full, split, D), (long long)workspace_bytes);
         n_full = nq;
         split = 1;
       }
@@ -1354,4 +1361,81 @@ extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t 
     if (key_mask) return launch_flash<64, false, true>(p, st);
     return launch_flash<64, false, false>(p, st);
   }
+}
+
+extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t H, int64_t D,
+                                  int64_t q_bs, int64_t q_ls, int64_t q_hs, int64_t n_segments,
+                                  const void* const* k_ptrs, const void* const* v_ptrs,
+                                  const int64_t* seg_lens, int64_t k_bs, int64_t k_ls, int64_t k_hs,
+                                  int64_t v_bs, int64_t v_ls, int64_t v_hs, int64_t v_ds, int kv_dtype,
+                                  const float* const* k_scales, const float* const* v_scales,
+                                  int64_t sc_bs, int64_t sc_hs, int64_t frame_tokens,
+                                  const float* key_mask, int64_t mask_bs, void* out, int64_t o_bs,
+                                  int64_t o_ls, int64_t o_hs, float* lse, float scale,
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
+  clear_error();
+  return flash_attn_fwd_impl(q, B, Lq, H, D, q_bs, q_ls, q_hs, n_segments, k_ptrs, v_ptrs, seg_lens, k_bs,
+                             k_ls, k_hs, v_bs, v_ls, v_hs, v_ds, kv_dtype, k_scales, v_scales, sc_bs, sc_hs,
+                             frame_tokens, key_mask, mask_bs, out, o_bs, o_ls, o_hs, lse, scale, workspace,
+                             workspace_bytes, false, stream);
+}
+
+// ---------------------------------------------------------------------------
+// No-allocation variant: the split partials live in a fixed device array.
+//
+// `scratch` holds the partial results of the split tail q-tiles (per piece:
+// 128 rows of (max, sum) in float32 and an O row in bf16).  The pieces of a
+// tail q-tile are at most the device's resident workgroups (tail x split <=
+// slots), so a call needs at most slots x 128 x (8 + 2 D) bytes: 17.3 MB for
+// D = 128 at 512 slots.  Every piece writes its whole partial before the
+// combine kernel reads it, so nothing needs clearing between calls.  Each
+// device holds its own copy of the array for the life of the process; its
+// device address is looked up once per device (hipGetSymbolAddress) and
+// only that address is handed to kernels.  Calls that overlap in time on one
+// device share the array and race.
+// ---------------------------------------------------------------------------
+constexpr int64_t kScratchBytes = LTX_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+// The current device's address of `scratch` (nullptr and an error message on failure).
+static void* scratch_for_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("ltx_flash_attn_fwd_noalloc: no current HIP device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      set_error("ltx_flash_attn_fwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+extern "C" int ltx_flash_attn_fwd_noalloc(const void* q, int64_t B, int64_t Lq, int64_t H, int64_t D,
+                                          int64_t q_bs, int64_t q_ls, int64_t q_hs, int64_t n_segments,
+                                          const void* const* k_ptrs, const void* const* v_ptrs,
+                                          const int64_t* seg_lens, int64_t k_bs, int64_t k_ls, int64_t k_hs,
+                                          int64_t v_bs, int64_t v_ls, int64_t v_hs, int64_t v_ds,
+                                          int kv_dtype, const float* const* k_scales,
+                                          const float* const* v_scales, int64_t sc_bs, int64_t sc_hs,
+                                          int64_t frame_tokens, const float* key_mask, int64_t mask_bs,
+                                          void* out, int64_t o_bs, int64_t o_ls, int64_t o_hs, float* lse,
+                                          float scale, void* stream) {
+  clear_error();
+  void* ws = scratch_for_current_device();
+  if (ws == nullptr) return LTX_ELAUNCH;
+  return flash_attn_fwd_impl(q, B, Lq, H, D, q_bs, q_ls, q_hs, n_segments, k_ptrs, v_ptrs, seg_lens, k_bs,
+                             k_ls, k_hs, v_bs, v_ls, v_hs, v_ds, kv_dtype, k_scales, v_scales, sc_bs, sc_hs,
+                             frame_tokens, key_mask, mask_bs, out, o_bs, o_ls, o_hs, lse, scale, ws,
+                             kScratchBytes, true, stream);
 }

@@ -264,8 +264,11 @@ class KVSegment:
 
 def flash_attn(q: torch.Tensor, segments: List[KVSegment], out: torch.Tensor,
                key_mask: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
-               scale: Optional[float] = None, frame_tokens: int = 0) -> None:
-    """ltx_flash_attn_fwd.  q/out [B, Lq, H, D] bf16; key_mask float32 [B, Lk] additive."""
+               scale: Optional[float] = None, frame_tokens: int = 0, noalloc: bool = False) -> None:
+    """ltx_flash_attn_fwd.  q/out [B, Lq, H, D] bf16; key_mask float32 [B, Lk] additive.
+    ``noalloc`` calls ltx_flash_attn_fwd_noalloc instead: no workspace tensor,
+    the split partials go to the library's fixed per-device scratch array
+    (calls overlapping on one device race on it)."""
     _need_gpu(q, out, key_mask, lse)
     if q.dtype != torch.bfloat16 or out.dtype != torch.bfloat16:
         raise TypeError("flash_attn: q and out must be bf16")
@@ -323,21 +326,24 @@ def flash_attn(q: torch.Tensor, segments: List[KVSegment], out: torch.Tensor,
         mask_bs = 0 if key_mask.shape[0] == 1 else key_mask.stride(0)
     if lse is not None and (lse.dtype != torch.float32 or lse.shape != (B, H, Lq) or not lse.is_contiguous()):
         raise ValueError("flash_attn: lse must be contiguous float32 [B, H, Lq]")
-    ws, ws_bytes = _flash_workspace(q, B, Lq, H, D)
     kp = N.ptr_array([s.k.data_ptr() for s in segs])
     vp = N.ptr_array([s.v.data_ptr() for s in segs])
     lens = N.i64_array([s.k.shape[1] for s in segs])
     ksp = N.ptr_array([s.k_scales.data_ptr() for s in segs]) if fp8 else None
     vsp = N.ptr_array([s.v_scales.data_ptr() for s in segs]) if fp8 else None
-    N.call("ltx_flash_attn_fwd", q.data_ptr(), B, Lq, H, D, q.stride(0), q.stride(1), q.stride(2),
-           len(segs), ctypes.cast(kp, ctypes.c_void_p), ctypes.cast(vp, ctypes.c_void_p),
-           ctypes.cast(lens, ctypes.c_void_p), kst[0], kst[1], kst[2], vst[0], vst[1], vst[2], vst[3],
-           kv_code,
-           ctypes.cast(ksp, ctypes.c_void_p) if fp8 else None,
-           ctypes.cast(vsp, ctypes.c_void_p) if fp8 else None, sc_bs, sc_hs,
-           int(frame_tokens), _ptr(key_mask), mask_bs, out.data_ptr(), out.stride(0), out.stride(1),
-           out.stride(2), _ptr(lse), float(scale) if scale is not None else 0.0, _ptr(ws), ws_bytes,
-           _stream(q))
+    args = (q.data_ptr(), B, Lq, H, D, q.stride(0), q.stride(1), q.stride(2),
+            len(segs), ctypes.cast(kp, ctypes.c_void_p), ctypes.cast(vp, ctypes.c_void_p),
+            ctypes.cast(lens, ctypes.c_void_p), kst[0], kst[1], kst[2], vst[0], vst[1], vst[2], vst[3],
+            kv_code,
+            ctypes.cast(ksp, ctypes.c_void_p) if fp8 else None,
+            ctypes.cast(vsp, ctypes.c_void_p) if fp8 else None, sc_bs, sc_hs,
+            int(frame_tokens), _ptr(key_mask), mask_bs, out.data_ptr(), out.stride(0), out.stride(1),
+            out.stride(2), _ptr(lse), float(scale) if scale is not None else 0.0)
+    if noalloc:
+        N.call("ltx_flash_attn_fwd_noalloc", *args, _stream(q))
+        return
+    ws, ws_bytes = _flash_workspace(q, B, Lq, H, D)
+    N.call("ltx_flash_attn_fwd", *args, _ptr(ws), ws_bytes, _stream(q))
 
 
 def adaln(x: torch.Tensor, y: Optional[torch.Tensor] = None, gate: Optional[torch.Tensor] = None,

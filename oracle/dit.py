@@ -25,6 +25,7 @@ import torch
 import torch.nn.functional as F
 
 from . import attention as OA
+from . import cache as OC
 
 
 def rms_norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
@@ -124,7 +125,9 @@ def block_forward(p: Dict[str, torch.Tensor], prefix: str, cfg, vx, ax, v_ts, a_
                   a_ss, a_gate, cache: Dict[str, Optional[torch.Tensor]], video_memory=None, audio_memory=None,
                   color_memory=None):
     """kv_cache.py:2145-2656, synchronous branch.  ``cache`` holds dense
-    video_self_k/v, audio_self_k/v, a2v_k/v, v2a_k/v (or None).  Returns (vx, ax)."""
+    video_self_k/v, audio_self_k/v, a2v_k/v, v2a_k/v (or None).  Returns
+    (vx, ax, new_cache): new_cache holds each field with this chunk's K/V
+    appended (the cache update of kv_cache.py:2642-2656, _cat_cache :394-398)."""
     eps = cfg.norm_eps
     B = vx.shape[0]
     vh, vdh, ah, adh = cfg.video_heads, cfg.video_d_head, cfg.audio_heads, cfg.audio_d_head
@@ -133,17 +136,18 @@ def block_forward(p: Dict[str, torch.Tensor], prefix: str, cfg, vx, ax, v_ts, a_
     a_steps = _memory_steps(p, prefix, cfg, "audio", audio_memory, None)
     t = lambda n: p[prefix + n]
     sh, sc, g = ada_values(t("scale_shift_table"), B, v_ts, slice(0, 3))
-    out, _, _ = OA.attention_with_cache(attn_weights(p, prefix + "attn1.", vh, vdh), rms_norm(vx, eps) * (1 + sc) + sh,
-                                        None, video_pe, None, cache.get("video_self_k"), cache.get("video_self_v"))
+    out, vs_k, vs_v = OA.attention_with_cache(attn_weights(p, prefix + "attn1.", vh, vdh),
+                                              rms_norm(vx, eps) * (1 + sc) + sh, None, video_pe, None,
+                                              cache.get("video_self_k"), cache.get("video_self_v"))
     vx = vx + out * g
     if mode == "memory_kv_side_branch":
         vx = _apply_steps(vx, v_steps, eps)
     v_text = OA.text_cross_attention(attn_weights(p, prefix + "attn2.", vh, vdh), rms_norm(vx, eps), video_ctx,
                                      video_mask)
     sh, sc, g = ada_values(t("audio_scale_shift_table"), B, a_ts, slice(0, 3))
-    out, _, _ = OA.attention_with_cache(attn_weights(p, prefix + "audio_attn1.", ah, adh),
-                                        rms_norm(ax, eps) * (1 + sc) + sh, None, audio_pe, None,
-                                        cache.get("audio_self_k"), cache.get("audio_self_v"))
+    out, as_k, as_v = OA.attention_with_cache(attn_weights(p, prefix + "audio_attn1.", ah, adh),
+                                              rms_norm(ax, eps) * (1 + sc) + sh, None, audio_pe, None,
+                                              cache.get("audio_self_k"), cache.get("audio_self_v"))
     ax = ax + out * g
     if mode == "memory_kv_side_branch":
         ax = _apply_steps(ax, a_steps, eps)
@@ -159,11 +163,11 @@ def block_forward(p: Dict[str, torch.Tensor], prefix: str, cfg, vx, ax, v_ts, a_
                                                                      a_gate)
     sc_v_a2v, sh_v_a2v, sc_v_v2a, sh_v_v2a, gate_a2v = av_ca_values(t("scale_shift_table_a2v_ca_video"), B, v_ss,
                                                                      v_gate)
-    a2v, _, _ = OA.attention_with_cache(attn_weights(p, prefix + "audio_to_video_attn.", ah, adh),
+    a2v, a2v_k, a2v_v = OA.attention_with_cache(attn_weights(p, prefix + "audio_to_video_attn.", ah, adh),
                                         vn * (1 + sc_v_a2v) + sh_v_a2v, an * (1 + sc_a_a2v) + sh_a_a2v,
                                         video_cross_pe, audio_cross_pe, cache.get("a2v_k"), cache.get("a2v_v"))
     vx = vx + a2v * gate_a2v
-    v2a, _, _ = OA.attention_with_cache(attn_weights(p, prefix + "video_to_audio_attn.", ah, adh),
+    v2a, v2a_k, v2a_v = OA.attention_with_cache(attn_weights(p, prefix + "video_to_audio_attn.", ah, adh),
                                         an * (1 + sc_a_v2a) + sh_a_v2a, vn * (1 + sc_v_v2a) + sh_v_v2a,
                                         audio_cross_pe, video_cross_pe, cache.get("v2a_k"), cache.get("v2a_v"))
     ax = ax + v2a * gate_v2a
@@ -171,26 +175,44 @@ def block_forward(p: Dict[str, torch.Tensor], prefix: str, cfg, vx, ax, v_ts, a_
     vx = vx + feed_forward(p, prefix + "ff.", rms_norm(vx, eps) * (1 + sc) + sh) * g
     sh, sc, g = ada_values(t("audio_scale_shift_table"), B, a_ts, slice(3, 6))
     ax = ax + feed_forward(p, prefix + "audio_ff.", rms_norm(ax, eps) * (1 + sc) + sh) * g
-    return vx, ax
+    new = {"video_self_k": vs_k, "video_self_v": vs_v, "audio_self_k": as_k, "audio_self_v": as_v,
+           "a2v_k": a2v_k, "a2v_v": a2v_v, "v2a_k": v2a_k, "v2a_v": v2a_v}
+    return vx, ax, {f: OC.cat_cache(cache.get(f), t) for f, t in new.items()}
+
+
+def per_token(t: torch.Tensor, tokens: int) -> torch.Tensor:
+    """_expand_per_frame_to_per_token (causal_model.py:1365-1392): [B, F, X] rows
+    of F equal frames repeated over their tokens; [B, 1, X] and one row per
+    token stay as they are."""
+    B, F_, X = t.shape
+    if F_ <= 1 or F_ == tokens:
+        return t
+    return t[:, :, None, :].expand(B, F_, tokens // F_, X).reshape(B, tokens, X)
 
 
 def forward_chunk(p: Dict[str, torch.Tensor], cfg, video_latent, audio_latent, sigma, video_ctx, audio_ctx,
                   video_mask, audio_mask, video_pe, audio_pe, video_cross_pe, audio_cross_pe,
                   caches: List[Dict[str, Optional[torch.Tensor]]], learned_memory_video=None,
-                  learned_memory_audio=None, learned_memory_color=None) -> Tuple[torch.Tensor, torch.Tensor]:
+                  learned_memory_audio=None, learned_memory_color=None, audio_sigma=None,
+                  return_caches: bool = False):
     """One denoising step: patchify, timestep modulation (causal_model.py:426-496),
-    the block loop, the output heads (causal_model.py:568-599)."""
+    the block loop, the output heads (causal_model.py:568-599).  ``sigma`` is
+    [B] or per latent frame [B, F] (expanded to the frames' tokens,
+    kv_cache.py:2895-2903); ``audio_sigma`` defaults to ``sigma``.  Returns
+    (video, audio) outputs, and with ``return_caches`` also every layer's cache
+    with the chunk appended."""
     B = video_latent.shape[0]
     vx = F.linear(video_latent, p["patchify_proj.weight"], p["patchify_proj.bias"])
     ax = F.linear(audio_latent, p["audio_patchify_proj.weight"], p["audio_patchify_proj.bias"])
     s = (sigma * cfg.timestep_scale_multiplier).flatten()
+    sa = ((sigma if audio_sigma is None else audio_sigma) * cfg.timestep_scale_multiplier).flatten()
     factor = cfg.av_ca_timestep_scale_multiplier / cfg.timestep_scale_multiplier
     v_ts, v_emb = adaln_single(p, "adaln_single.", s)
-    a_ts, a_emb = adaln_single(p, "audio_adaln_single.", s)
+    a_ts, a_emb = adaln_single(p, "audio_adaln_single.", sa)
     v_ss, _ = adaln_single(p, "av_ca_video_scale_shift_adaln_single.", s)
-    a_ss, _ = adaln_single(p, "av_ca_audio_scale_shift_adaln_single.", s)
+    a_ss, _ = adaln_single(p, "av_ca_audio_scale_shift_adaln_single.", sa)
     v_gate, _ = adaln_single(p, "av_ca_a2v_gate_adaln_single.", s * factor)
-    a_gate, _ = adaln_single(p, "av_ca_v2a_gate_adaln_single.", s * factor)
+    a_gate, _ = adaln_single(p, "av_ca_v2a_gate_adaln_single.", sa * factor)
     vm = am = cm = None
     if getattr(cfg, "learned_memory_enabled", False):
         if learned_memory_video is not None:
@@ -201,13 +223,16 @@ def forward_chunk(p: Dict[str, torch.Tensor], cfg, video_latent, audio_latent, s
                           p["learned_memory_audio_encoder.bias"])
         if learned_memory_color is not None and cfg.learned_memory_color_film_enabled:
             cm = learned_memory_color
-    view = lambda x: x.view(B, -1, x.shape[-1])
-    v_ts, v_emb, a_ts, a_emb = view(v_ts), view(v_emb), view(a_ts), view(a_emb)
-    v_ss, a_ss, v_gate, a_gate = view(v_ss), view(a_ss), view(v_gate), view(a_gate)
+    vview = lambda x: per_token(x.view(B, -1, x.shape[-1]), vx.shape[1])
+    aview = lambda x: per_token(x.view(B, -1, x.shape[-1]), ax.shape[1])
+    v_ts, v_emb, a_ts, a_emb = vview(v_ts), vview(v_emb), aview(a_ts), aview(a_emb)
+    v_ss, a_ss, v_gate, a_gate = vview(v_ss), aview(a_ss), vview(v_gate), aview(a_gate)
+    new_caches = []
     for i in range(cfg.num_layers):
-        vx, ax = block_forward(p, f"transformer_blocks.{i}.", cfg, vx, ax, v_ts, a_ts, video_pe, audio_pe,
-                               video_cross_pe, audio_cross_pe, video_ctx, audio_ctx, video_mask, audio_mask,
-                               v_ss, v_gate, a_ss, a_gate, caches[i], vm, am, cm)
+        vx, ax, nc = block_forward(p, f"transformer_blocks.{i}.", cfg, vx, ax, v_ts, a_ts, video_pe, audio_pe,
+                                   video_cross_pe, audio_cross_pe, video_ctx, audio_ctx, video_mask, audio_mask,
+                                   v_ss, v_gate, a_ss, a_gate, caches[i], vm, am, cm)
+        new_caches.append(nc)
 
     def head(table, proj, x, emb):
         v = table[None, None] + emb[:, :, None]
@@ -215,5 +240,6 @@ def forward_chunk(p: Dict[str, torch.Tensor], cfg, video_latent, audio_latent, s
         return F.linear(F.layer_norm(x, (x.shape[-1],), eps=1e-6) * (1 + scale) + shift, p[proj + ".weight"],
                         p[proj + ".bias"])
 
-    return (head(p["scale_shift_table"], "proj_out", vx, v_emb),
-            head(p["audio_scale_shift_table"], "audio_proj_out", ax, a_emb))
+    out = (head(p["scale_shift_table"], "proj_out", vx, v_emb),
+           head(p["audio_scale_shift_table"], "audio_proj_out", ax, a_emb))
+    return (*out, new_caches) if return_caches else out

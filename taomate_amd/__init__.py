@@ -9,6 +9,8 @@ The public names mirror the reference's drop-in surface:
   (ltx_causal/rope/causal_rope.py:45-357)
 * ``LayerKVCache``, ``KVCache``, ``init_kv_cache``, ``_cat_cache``
   (ltx_causal/transformer/kv_cache.py:321-398, ltx_causal/wrapper.py:15)
+* ``install`` rebinds those names inside a running TaoMate process wherever its
+  modules hold them, and replaces the wrapper's ``init_kv_cache()``
 * ``retain_streaming_context``, ``cache_segments``, ``attach_segments``
   (taomate/inference/cache.py), ``compute_av_blocks`` (mask_builder.py:102)
 * ``LearnedMemoryState``, ``StreamingMemory`` (taomate/runtime_support/learned_memory.py,
@@ -26,7 +28,8 @@ from .blocks import AVBlock, compute_aligned_audio_frames, compute_av_blocks, gl
 from .cache import (attach_segments, cache_segments, prune_clean_kv_to_sink_recent,
                     retain_streaming_context)
 from .kv_cache import (ArenaSpec, KVArena, KVArenaFull, KVCache, KVSpanView, LayerKVCache,
-                       _cat_cache, init_kv_cache)
+                       _cat_cache, attach_arena, attach_block_arenas, init_kv_cache)
+from .integration import ArenaPlan, Installation, init_kv_cache_for, install
 from .rope import CausalRopeType, apply_split_rotary_emb, causal_precompute_freqs_cis, generate_freq_grid
 from .streaming import ChunkStream, retain_pinned_recent
 from .memory import LearnedMemoryState, StreamingMemory
@@ -42,5 +45,6 @@ __all__ = [
     "LayerKVCache", "_cat_cache", "init_kv_cache", "CausalRopeType", "apply_split_rotary_emb",
     "causal_precompute_freqs_cis", "generate_freq_grid", "ChunkStream", "retain_pinned_recent",
     "LearnedMemoryState", "StreamingMemory", "load_generator", "save_generator", "build_prefix_state_payload",
-    "load_prefix_state", "save_prefix_state",
+    "load_prefix_state", "save_prefix_state", "attach_arena", "attach_block_arenas", "ArenaPlan",
+    "Installation", "init_kv_cache_for", "install",
 ]

@@ -23,7 +23,7 @@ import torch.nn as nn
 
 from . import kernels
 from .kernels import KVSegment
-from .kv_cache import KVSpanView
+from .kv_cache import KVSpanView, module_arena
 from .rope import CausalRopeType, apply_split_rotary_emb
 
 
@@ -156,12 +156,20 @@ def _check_bf16(*ts):
             raise TypeError(f"the gfx950 attention path runs bf16 activations, got {t.dtype}")
 
 
-def _project_qkv(attn: CausalLTXAttention, x: torch.Tensor, ctx: torch.Tensor):
+def packed_qkv(attn: nn.Module) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
+    """The packed q/k/v (weight, bias) of a module packed by ``fuse_qkv_``;
+    None for any other module, including one built by the reference
+    (causal_attention.py:61-118), which carries only the three Linears."""
+    fn = getattr(attn, "_packed_qkv", None)
+    return fn() if fn is not None else None
+
+
+def _project_qkv(attn: nn.Module, x: torch.Tensor, ctx: torch.Tensor):
     """to_q(x), to_k(ctx), to_v(ctx) (kv_cache.py:1406-1408).  A self-attention
     packed by ``fuse_qkv_`` runs one GEMM and returns three column views of its
     [B, L, 3·inner] output (row stride 3·inner), which the norm / RoPE and
     append kernels read in place."""
-    packed = attn._packed_qkv() if ctx is x else None
+    packed = packed_qkv(attn) if ctx is x else None
     if packed is None:
         return attn.to_q(x), attn.to_k(ctx), attn.to_v(ctx)
     y = torch.nn.functional.linear(x, *packed)
@@ -360,7 +368,13 @@ def attention_with_cache(
     v_lin = v_lin[:, :real]
 
     arena = cached_k.arena if isinstance(cached_k, KVSpanView) else None
+    if cached_k is None and cached_v is None:
+        # an empty field of the reference's init_kv_cache(): a module with an
+        # arena plan starts its cache in that arena (None: dense tensors)
+        arena = module_arena(attn, B, x.device)
     segs, frame = _cached_segments(cached_k, cached_v)
+    if arena is not None and arena.fp8:
+        frame = arena.frame_tokens
     if arena is not None and not arena.fp8:
         slot = arena.alloc(real)
         k_dst = arena.slots("k", slot, real)

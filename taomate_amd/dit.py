@@ -293,11 +293,17 @@ def _apply_memory(x: torch.Tensor, n: Optional[torch.Tensor], steps, eps: float,
     return x, n
 
 
-def _all_blocks_ada(blocks, batch: int, v_ts, a_ts, v_ss, v_gate, a_ss, a_gate) -> List[Dict[str, tuple]]:
+def _all_blocks_ada(blocks, batch: int, v_ts, a_ts, v_ss, v_gate, a_ss, a_gate) -> List[Optional[Dict[str, tuple]]]:
     """Every block's modulation values (AVBlock.get_ada_values /
     get_av_ca_ada_values, causal_block.py:434-481) with one add per table kind
     over the stacked tables of all blocks instead of eight small adds per
-    block: the same elementwise table + timestep sums."""
+    block: the same elementwise table + timestep sums.  Only for one timestep
+    row per sample ([B, 1, n*D]): with per-token rows the stacked values of all
+    blocks would be [L, B, T, n, D] at once (gigabytes at a 1152-token chunk),
+    so each block then computes its own inside the block loop (None here)."""
+    if any(t.shape[1] != 1 for t in (v_ts, a_ts, v_ss, v_gate, a_ss, a_gate)):
+        return [None] * len(blocks)
+
     def stacked(name, ts, rows):
         tab = torch.stack([getattr(b, name)[rows] for b in blocks]).to(device=ts.device, dtype=ts.dtype)
         n = tab.shape[1]
@@ -421,6 +427,13 @@ class AVModel(nn.Module):
         self.audio_norm_out = nn.LayerNorm(ad, elementwise_affine=False, eps=1e-6)
         self.audio_proj_out = nn.Linear(ad, cfg.out_channels)
 
+    def init_kv_cache(self, plan=None):
+        """CausalLTX2DiffusionWrapper.init_kv_cache (wrapper.py:15-20): an empty
+        LayerKVCache per block.  With an ``integration.ArenaPlan`` every block's
+        four cached attentions start their caches in arenas of that size."""
+        from .integration import init_kv_cache_for
+        return init_kv_cache_for(self, plan)
+
     def fuse_qkv_(self) -> "AVModel":
         """Pack the q/k/v projections of every self-attention (video and audio)
         into one GEMM each; parameter names, values and memory are unchanged
@@ -438,6 +451,18 @@ class AVModel(nn.Module):
             blk.attn2.cache_text_kv_(enabled, size)
             blk.audio_attn2.cache_text_kv_(enabled, size)
         return self
+
+    @staticmethod
+    def _per_token(t: torch.Tensor, tokens: int) -> torch.Tensor:
+        """_expand_per_frame_to_per_token (causal_model.py:1365-1392): [B, F, X]
+        per-frame rows repeated over the F equal frames of ``tokens`` tokens;
+        one row ([B, 1, X]) broadcasts and stays as it is."""
+        B, F, X = t.shape
+        if F <= 1 or F == tokens:
+            return t
+        if tokens % F:
+            raise ValueError(f"{tokens} tokens are not {F} equal frames")
+        return t.unsqueeze(2).expand(B, F, tokens // F, X).reshape(B, tokens, X)
 
     def _timestep(self, sigma: torch.Tensor, adaln: AdaLayerNormSingle, batch: int, dtype):
         """causal_model.py:426-455."""
@@ -466,11 +491,17 @@ class AVModel(nn.Module):
                       caches: List[LayerKVCache], commit: bool = False,
                       learned_memory_video: Optional[torch.Tensor] = None,
                       learned_memory_audio: Optional[torch.Tensor] = None,
-                      learned_memory_color: Optional[torch.Tensor] = None, kv_cache_only: bool = False):
+                      learned_memory_color: Optional[torch.Tensor] = None, kv_cache_only: bool = False,
+                      audio_sigma: Optional[torch.Tensor] = None):
         """One denoising step of a chunk (the block loop of
         model_forward_inference, kv_cache.py:2681-3365): returns the video and
         audio outputs [B, T, out_channels] and, with ``commit``, the caches
         with the chunk's keys appended (a denoise step leaves them as given).
+        ``sigma`` is one value per sample [B] or one per latent frame [B, F]
+        (the reference's ``timesteps``; a conditioning frame carries 0,
+        model_runtime.py:897-910), expanded to the frame's tokens
+        (kv_cache.py:2895-2903); ``audio_sigma`` ([B] or one per audio token)
+        defaults to ``sigma`` when that is per sample.
         The learned-memory tensors ([B, N, in_channels] tokens, [B, 4C] colour
         vector, from ``LearnedMemoryState.with_conditional_memory``) are used
         when the model has memory adapters.  ``kv_cache_only`` is the clean
@@ -490,12 +521,19 @@ class AVModel(nn.Module):
                 cm = learned_memory_color.to(device=dev, dtype=dt)
         vx = self.patchify_proj(video_latent)
         ax = self.audio_patchify_proj(audio_latent)
+        if audio_sigma is None:
+            if sigma.dim() == 2 and sigma.shape[1] > 1:
+                raise ValueError("per-frame video sigma needs its own audio_sigma ([B] or [B, audio tokens])")
+            audio_sigma = sigma
+        Lv, La = vx.shape[1], ax.shape[1]
         v_ts, v_emb = self._timestep(sigma, self.adaln_single, B, dt)
-        a_ts, a_emb = self._timestep(sigma, self.audio_adaln_single, B, dt)
+        a_ts, a_emb = self._timestep(audio_sigma, self.audio_adaln_single, B, dt)
         v_ss, v_gate = self._cross_timestep(sigma, self.av_ca_video_scale_shift_adaln_single,
                                             self.av_ca_a2v_gate_adaln_single, B, dt)
-        a_ss, a_gate = self._cross_timestep(sigma, self.av_ca_audio_scale_shift_adaln_single,
+        a_ss, a_gate = self._cross_timestep(audio_sigma, self.av_ca_audio_scale_shift_adaln_single,
                                             self.av_ca_v2a_gate_adaln_single, B, dt)
+        v_ts, v_emb, v_ss, v_gate = (self._per_token(t, Lv) for t in (v_ts, v_emb, v_ss, v_gate))
+        a_ts, a_emb, a_ss, a_gate = (self._per_token(t, La) for t in (a_ts, a_emb, a_ss, a_gate))
         new_caches = []
         ada = _all_blocks_ada(self.transformer_blocks, B, v_ts, a_ts, v_ss, v_gate, a_ss, a_gate)
         for blk, cache, blk_ada in zip(self.transformer_blocks, caches, ada):

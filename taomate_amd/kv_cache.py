@@ -326,3 +326,81 @@ def init_kv_cache(num_layers: int, batch: int, specs: Dict[str, ArenaSpec],
             kw[fv] = arena.empty_view("v")
         layers.append(LayerKVCache(**kw))
     return KVCache(layers=layers)
+
+
+# ---------------------------------------------------------------------------
+# Arenas attached to attention modules.
+#
+# The reference starts every stream from ``init_kv_cache()`` with no
+# arguments (wrapper.py:15-20): each LayerKVCache field is None until the
+# first append.  An attention module that carries an arena plan gets its own
+# KVArena, created on its first call (the batch and device come from that
+# call), so the first append of a None field already lands in arena slots and
+# every later cache of that field is a KVSpanView of it.
+# ---------------------------------------------------------------------------
+
+def attach_arena(attn, capacity: int, kv_dtype: str = "bf16", frame_tokens: int = 1, name: str = "") -> None:
+    """Give ``attn`` (any module with ``heads`` / ``dim_head``) an arena plan of
+    ``capacity`` tokens; the arena itself is allocated on first use."""
+    if kv_dtype not in ("bf16", "fp8"):
+        raise ValueError(f"kv_dtype must be 'bf16' or 'fp8', got {kv_dtype!r}")
+    attn.__dict__["_ltx_arena_plan"] = ArenaSpec(int(capacity), int(attn.heads), int(attn.dim_head), kv_dtype,
+                                                 int(frame_tokens))
+    attn.__dict__["_ltx_arena_name"] = name
+    attn.__dict__.pop("_ltx_arena", None)
+
+
+def detach_arena(attn) -> None:
+    for k in ("_ltx_arena_plan", "_ltx_arena_name", "_ltx_arena"):
+        attn.__dict__.pop(k, None)
+
+
+def module_arena(attn, batch: int, device) -> Optional[KVArena]:
+    """The arena of ``attn`` for this batch and device (created on first use,
+    replaced when either changes; views of the old arena keep it alive), or
+    None when ``attn`` carries no plan."""
+    spec = attn.__dict__.get("_ltx_arena_plan")
+    if spec is None:
+        return None
+    dev = torch.device(device)
+    arena = attn.__dict__.get("_ltx_arena")
+    if arena is None or arena.B != int(batch) or arena.device != dev:
+        arena = KVArena(batch, spec.capacity, spec.heads, spec.dim_head, dev, spec.kv_dtype, spec.frame_tokens,
+                        name=attn.__dict__.get("_ltx_arena_name", ""))
+        attn.__dict__["_ltx_arena"] = arena
+    return arena
+
+
+# attention module of each cached kind in a dual-stream block
+# (causal_block.py:260-376): its keys/values come from the stream named
+BLOCK_CACHE_MODULES = {
+    "video_self": ("attn1", "video"),
+    "audio_self": ("audio_attn1", "audio"),
+    "a2v": ("audio_to_video_attn", "audio"),
+    "v2a": ("video_to_audio_attn", "video"),
+}
+
+
+def attach_block_arenas(blocks, video_tokens: int, audio_tokens: int, kv_dtype: str = "bf16",
+                        video_frame_tokens: int = 1) -> None:
+    """Arena plans for the four cached attentions of every block: video-keyed
+    kinds (video_self, v2a) hold ``video_tokens``, audio-keyed kinds
+    (audio_self, a2v) ``audio_tokens``.  ``kv_dtype`` "fp8" applies to the
+    video-keyed kinds (frame-aligned appends of ``video_frame_tokens``); the
+    audio kinds stay bf16 (audio latent frames are single tokens)."""
+    for i, blk in enumerate(blocks):
+        for kind, (attr, stream) in BLOCK_CACHE_MODULES.items():
+            attn = getattr(blk, attr, None)
+            if attn is None:
+                continue
+            if stream == "video":
+                attach_arena(attn, video_tokens, kv_dtype, video_frame_tokens if kv_dtype == "fp8" else 1,
+                             name=f"layer{i}.{kind}")
+            else:
+                attach_arena(attn, audio_tokens, "bf16", 1, name=f"layer{i}.{kind}")
+
+
+def empty_kv_cache(num_layers: int) -> KVCache:
+    """The reference's empty cache (wrapper.py:15-20): one LayerKVCache with
+    every field None per layer."""
+    return KVCache(layers=[LayerKVCache() for _ in range(int(num_layers))])

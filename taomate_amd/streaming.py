@@ -31,7 +31,7 @@ from typing import Dict, List, Optional, Tuple
 import torch
 
 from . import kernels
-from .attention import CausalLTXAttention, _check_bf16, attention_with_cache
+from .attention import CausalLTXAttention, _check_bf16, attention_with_cache, packed_qkv
 from .cache import _segment_offsets, _slice_tensor
 from .kv_cache import KVArena, KVSpanView, _cat_cache
 from .rope import causal_precompute_freqs_cis
@@ -54,7 +54,7 @@ def prefill_kv(attn: CausalLTXAttention, x: torch.Tensor, pe, arena: KVArena) ->
     a segment, with no attention output."""
     B, L, _ = x.shape
     H, D = attn.heads, attn.dim_head
-    packed = attn._packed_qkv()
+    packed = packed_qkv(attn)
     if packed is None:
         k_lin, v_lin = attn.to_k(x), attn.to_v(x)
     else:   # the K and V rows of a packed q/k/v weight (fuse_qkv_): one GEMM

@@ -4,6 +4,7 @@ packing keeps every parameter's name and value, the one GEMM equals the three
 packing instead of leaving the GEMM on stale weights."""
 import os
 
+import pytest
 import torch
 
 import taomate_amd as T
@@ -96,7 +97,7 @@ def test_all_blocks_modulation_equals_per_block():
     with torch.no_grad():
         for p in model.parameters():
             p.normal_()
-    B, T = 2, 3
+    B, T = 2, 1
     r = lambda *s: torch.randn(*s).to(torch.bfloat16)
     v_ts, a_ts = r(B, T, 6 * 128), r(B, T, 6 * 64)
     v_ss, v_gate, a_ss, a_gate = r(B, T, 4 * 128), r(B, T, 128), r(B, T, 4 * 64), r(B, T, 64)
@@ -113,3 +114,33 @@ def test_all_blocks_modulation_equals_per_block():
         assert all(torch.equal(g_, w_) for g_, w_ in zip(got["v"][3:6],
                                                          blk.get_ada_values(blk.scale_shift_table, B, v_ts,
                                                                             slice(3, 6))))
+
+
+def test_per_token_modulation_is_not_stacked_over_blocks():
+    """With per-token timestep rows (a per-frame sigma expanded to the chunk's
+    tokens) the values of all blocks are not built at once: _all_blocks_ada
+    hands every block None, and each block's own get_ada_values gives the
+    per-token values."""
+    cfg = D.AVConfig(num_layers=2, video_dim=128, audio_dim=64, video_heads=2, audio_heads=1, video_d_head=64,
+                     audio_d_head=64, in_channels=8)
+    model = D.AVModel(cfg).to(torch.bfloat16)
+    B, T = 2, 12
+    r = lambda *s: torch.randn(*s).to(torch.bfloat16)
+    ts = [r(B, T, 6 * 128), r(B, T, 6 * 64), r(B, T, 4 * 128), r(B, T, 128), r(B, T, 4 * 64), r(B, T, 64)]
+    assert D._all_blocks_ada(model.transformer_blocks, B, *ts) == [None, None]
+
+
+def test_per_frame_sigma_expands_to_tokens():
+    """_expand_per_frame_to_per_token (causal_model.py:1365-1392): each frame's
+    row repeated over its tokens; one row, or one row per token, unchanged."""
+    t = torch.arange(2 * 3 * 4, dtype=torch.float32).view(2, 3, 4)
+    e = D.AVModel._per_token(t, 12)
+    assert e.shape == (2, 12, 4)
+    for f in range(3):
+        for i in range(4):
+            assert torch.equal(e[:, 4 * f + i], t[:, f])
+    assert D.AVModel._per_token(t, 3) is t
+    one = t[:, :1]
+    assert D.AVModel._per_token(one, 12) is one
+    with pytest.raises(ValueError):
+        D.AVModel._per_token(t, 10)

@@ -184,3 +184,57 @@ def test_ffn_gelu_epilogue(dev, L):
     e_two = (two.float() - ref).abs()
     assert e_epi.max().item() <= 2e-2 and e_epi.mean().item() <= 2e-3
     assert e_epi.mean().item() <= e_two.mean().item() * 1.05
+
+
+def _arena_caches(dev, cfg, dense_caches):
+    """The dense per-layer caches copied into one arena per layer and kind,
+    with room for two more chunks."""
+    hw = GH * GW
+    specs = {"video_self": T.ArenaSpec((NCACHE_F + 2 * NF) * hw, cfg.video_heads, cfg.video_d_head),
+             "audio_self": T.ArenaSpec(LA_CACHE + 2 * LA + 8, cfg.audio_heads, cfg.audio_d_head)}
+    kvc = T.init_kv_cache(cfg.num_layers, B, specs, dev)
+    caches = []
+    for lay, c in zip(kvc.layers, dense_caches):
+        va, aa = lay.video_self_k.arena, lay.audio_self_k.arena
+        nv, na = c["video_self_k"].shape[1], c["audio_self_k"].shape[1]
+        for arena, n, kk, vv in ((va, nv, "video_self_k", "video_self_v"), (aa, na, "audio_self_k", "audio_self_v")):
+            arena.slots("k", 0, n).copy_(c[kk].to(dev, torch.bfloat16))
+            arena.slots("v", 0, n).copy_(c[vv].to(dev, torch.bfloat16))
+        caches.append(T.LayerKVCache(video_self_k=KVSpanView(va, "k", [(0, nv)]),
+                                     video_self_v=KVSpanView(va, "v", [(0, nv)]),
+                                     audio_self_k=KVSpanView(aa, "k", [(0, na)]),
+                                     audio_self_v=KVSpanView(aa, "v", [(0, na)])))
+    return caches
+
+
+def test_per_frame_sigma_matches_oracle(dev):
+    """One sigma per latent frame with frame 1 a clean conditioning frame
+    (sigma 0, model_runtime.py:897-910), expanded over the frame's tokens
+    (kv_cache.py:2895-2903), and a per-sample audio sigma, against the oracle."""
+    model = D.build_model(CFG, dev, seed=3)
+    params = {n: p.detach().float().cpu() for n, p in model.named_parameters()}
+    x = _inputs()
+    g = torch.Generator().manual_seed(9)
+    sigma = torch.rand(B, NF, generator=g)
+    sigma[:, 1] = 0.0
+    a_sigma = torch.rand(B, generator=g)
+    ref_v, ref_a = OD.forward_chunk(params, CFG, x["video"], x["audio"], sigma, x["vctx"], x["actx"],
+                                    x["mask"].float(), x["mask"].float(), *_pes(), x["cache"], audio_sigma=a_sigma)
+    # the conditioning frame changes the result: per-frame sigma is not the per-sample one
+    ref_u, _ = OD.forward_chunk(params, CFG, x["video"], x["audio"], sigma[:, 0], x["vctx"], x["actx"],
+                                x["mask"].float(), x["mask"].float(), *_pes(), x["cache"], audio_sigma=a_sigma)
+    assert (ref_u - ref_v).abs().max().item() > 1e-2
+    caches = _arena_caches(dev, CFG, x["cache"])
+    bf = lambda t: t.to(dev, torch.bfloat16)
+    with torch.no_grad():
+        vo, ao, _ = model.forward_chunk(bf(x["video"]), bf(x["audio"]), sigma.to(dev), bf(x["vctx"]), bf(x["actx"]),
+                                        bf(x["mask"]), bf(x["mask"]), *_pes(dev), caches, audio_sigma=a_sigma.to(dev))
+        with pytest.raises(ValueError, match="audio_sigma"):
+            model.forward_chunk(bf(x["video"]), bf(x["audio"]), sigma.to(dev), bf(x["vctx"]), bf(x["actx"]),
+                                bf(x["mask"]), bf(x["mask"]), *_pes(dev), caches)
+    torch.cuda.synchronize()
+    cv, ca = cosine(vo, ref_v), cosine(ao, ref_a)
+    assert cv >= 0.999 and ca >= 0.999, (cv, ca)
+    for out, ref in ((vo, ref_v), (ao, ref_a)):
+        err = (out.float().cpu() - ref).abs().max().item()
+        assert err <= 3e-2 * ref.abs().max().item(), err

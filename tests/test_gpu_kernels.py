@@ -1,4 +1,5 @@
 """GPU parity of each kernel against the CPU oracle (run on an MI355X)."""
+import ctypes
 import math
 
 import pytest
@@ -7,7 +8,7 @@ import torch
 from oracle import attention as OA
 from oracle import fp8 as OF
 from oracle import rope as OR
-from taomate_amd import kernels
+from taomate_amd import _native, kernels
 from taomate_amd.kernels import KVSegment
 from taomate_amd.rope import causal_precompute_freqs_cis, generate_freq_grid
 
@@ -564,3 +565,34 @@ def test_adaln_matches_torch_ops(dev, C, L, per_row):
         exact = (out == ref).float().mean().item()
         d = (out.float() - ref.float()).abs().max().item()
         assert exact >= 0.995 and d <= 2 ** -6 * ref.float().abs().max().item(), (exact, d)
+
+
+@pytest.mark.parametrize("vlayout", ["token", "key"])
+def test_flash_attn_d64_split_tail(dev, vlayout):
+    """D = 64 with enough q-tiles to leave a partial last round (B=2, H=64,
+    1152 queries = 1152 q-tiles) and 32 key tiles, so the tail q-tiles are cut
+    into key ranges and merged by the D = 64 combine kernel; both V layouts
+    against fp32."""
+    B, Lq, H, D, lens = 2, 1152, 64, 64, [1024, 1024]
+    ws = ctypes.c_int64(0)
+    _native.call("ltx_flash_attn_workspace_size", B, Lq, H, D, ctypes.byref(ws))
+    assert ws.value > 0, "the shape must plan a split tail"
+    g = gen(17)
+    q = randn((B, Lq, H, D), g, torch.bfloat16)
+    ks = [randn((B, n, H, D), g, torch.bfloat16) for n in lens]
+    vs = [randn((B, n, H, D), g, torch.bfloat16) for n in lens]
+    cap = sum(lens) + 64
+    ka = torch.zeros(B, cap, H, D, dtype=torch.bfloat16, device=dev)
+    va = torch.zeros_like(ka) if vlayout == "token" else \
+        torch.zeros(B, H, D, cap, dtype=torch.bfloat16, device=dev).permute(0, 3, 1, 2)
+    segs, pos = [], 0
+    for kk, vv in zip(ks, vs):
+        n = kk.shape[1]
+        ka[:, pos:pos + n] = kk.to(dev)
+        va[:, pos:pos + n] = vv.to(dev)
+        segs.append(KVSegment(ka[:, pos:pos + n], va[:, pos:pos + n]))
+        pos += n + 32
+    out = torch.empty(B, Lq, H, D, dtype=torch.bfloat16, device=dev)
+    kernels.flash_attn(q.to(dev), segs, out)
+    torch.cuda.synchronize()
+    assert_bf16_close(out, _ref_attn(q, torch.cat(ks, 1), torch.cat(vs, 1)), f"D64 split tail {vlayout}")

@@ -13,9 +13,13 @@ The layout widens the reference's sink-plus-recent policy:
 * memory -- ``memory_frames`` frames at fixed positions right after the anchor,
   kind "memory", pinned, and re-prefilled every ``refresh_every`` chunks from
   an evolving state at those original positions (the re-prefill of retained
-  segments at their global positions, taomate/inference/runtime.py:386-470;
-  the state update stands in for the learned-memory EMA,
-  taomate/runtime_support/learned_memory.py:507-591);
+  segments at their global positions, taomate/inference/runtime.py:386-470).
+  The state evolves by the reference's memory rule, an EMA with an identity
+  tether (_ema_update, taomate/runtime_support/learned_memory.py:231-249):
+  state <- ((1 - beta) state + beta new) (1 - tether) + tether anchor, where
+  new is the newest chunk's last memory frames, anchor the state the stream
+  started from, and beta / tether the streaming settings 0.15 / 0.20
+  (video_beta, video_anchor_tether, taomate/inference/memory.py:4-29);
 * window -- the newest generated chunks whose frames fit in ``window_frames``;
 * current -- the chunk being generated (``chunk_frames`` frames).
 
@@ -82,7 +86,7 @@ class ChunkStream:
     def __init__(self, attn: CausalLTXAttention, video_hw: Tuple[int, int], batch: int, device="cuda",
                  anchor_frames: int = 1, memory_frames: int = 2, chunk_frames: int = 3,
                  window_frames: int = 12, refresh_every: int = 4, kv_dtype: str = "fp8",
-                 theta: float = 10000.0, memory_mix: float = 0.5):
+                 theta: float = 10000.0, memory_beta: float = 0.15, memory_tether: float = 0.20):
         if window_frames % chunk_frames:
             raise ValueError("window_frames must be a whole number of chunks")
         if kv_dtype == "fp8" and (int(video_hw[0]) * int(video_hw[1])) % 64:
@@ -98,7 +102,8 @@ class ChunkStream:
         self.recent = self.window_frames // self.chunk_frames
         self.refresh_every = int(refresh_every)
         self.theta = float(theta)
-        self.memory_mix = float(memory_mix)
+        self.memory_beta = min(max(float(memory_beta), 0.0), 1.0)
+        self.memory_tether = min(max(float(memory_tether), 0.0), 1.0)
         # live at most: anchor + two memory versions (during a swap) + window
         # + the chunk being committed and the next; one chunk of slack for
         # first-fit fragmentation
@@ -109,6 +114,7 @@ class ChunkStream:
         self.v: KVSpanView = self.arena.empty_view("v")
         self.segments: List[Dict] = []
         self.memory_state: Optional[torch.Tensor] = None
+        self.memory_anchor: Optional[torch.Tensor] = None
         self.memory_version = 0
         self.chunks_done = 0
         self._pe_cache: "OrderedDict[Tuple[int, int], tuple]" = OrderedDict()
@@ -164,17 +170,21 @@ class ChunkStream:
             if x_memory is None:
                 raise ValueError("memory frames configured but no memory hidden states given")
             self.memory_state = x_memory.float().clone()
+            self.memory_anchor = self.memory_state.clone()
             km, vm = self._prefill_segment(x_memory, self.anchor_frames, self.memory_frames)
             self.k, self.v = _cat_cache(self.k, km), _cat_cache(self.v, vm)
             self.segments.append(self._segment("memory", 1, self.memory_frames))
 
     def refresh_memory(self, x_recent: torch.Tensor) -> None:
-        """Evolve the fp32 memory state with the newest frames (state <- mix *
-        state + (1 - mix) * last memory_frames frames of ``x_recent``), re-prefill it at
-        the memory's own positions and swap it into the cache in place."""
+        """Evolve the fp32 memory state with the last memory_frames frames of
+        ``x_recent`` (EMA, then the tether to the starting state), re-prefill
+        it at the memory's own positions and swap it into the cache in place."""
         n = self.memory_frames * self.hw
         tail = x_recent[:, -n:]
-        self.memory_state = self.memory_state * self.memory_mix + tail.float() * (1.0 - self.memory_mix)
+        ema = self.memory_state * (1.0 - self.memory_beta) + tail.float() * self.memory_beta
+        if self.memory_tether > 0.0:
+            ema = ema * (1.0 - self.memory_tether) + self.memory_anchor * self.memory_tether
+        self.memory_state = ema
         km, vm = self._prefill_segment(self.memory_state.to(x_recent.dtype), self.anchor_frames,
                                        self.memory_frames)
         mi = next(i for i, s in enumerate(self.segments) if s["kind"] == "memory")

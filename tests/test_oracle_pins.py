@@ -283,3 +283,21 @@ def test_block_returns_the_committed_cache():
     assert c2["video_self_k"].shape == (1, 6, 2, 8)
     assert torch.equal(c2["video_self_k"][:, :3], c1["video_self_k"])
     assert torch.equal(c2["video_self_k"][:, 3:], c1["video_self_k"])   # same inputs, same keys
+
+
+def test_memory_ema_rule_special_cases():
+    """_ema_update (learned_memory.py:231-249): beta 0 keeps the state, beta 1
+    takes the new frames, tether 1 returns the anchor, and one step with the
+    streaming settings (0.15, 0.20) is the two-stage closed form; a tether
+    applied before the EMA (a plausible slip) differs."""
+    from oracle import stream as OS
+    g = torch.Generator().manual_seed(6)
+    prev, anchor, cur = (torch.randn(2, 5, 4, generator=g) for _ in range(3))
+    assert torch.equal(OS.ema_update(prev, None, cur, 0.0, 0.0), prev)
+    assert torch.equal(OS.ema_update(prev, None, cur, 1.0, 0.0), cur)
+    torch.testing.assert_close(OS.ema_update(prev, anchor, cur, 0.3, 1.0), anchor)
+    got = OS.ema_update(prev, anchor, cur, 0.15, 0.20)
+    want = 0.8 * (0.85 * prev + 0.15 * cur) + 0.2 * anchor
+    torch.testing.assert_close(got, want)
+    slip = 0.85 * (0.8 * prev + 0.2 * anchor) + 0.15 * cur
+    assert (got - slip).abs().max().item() > 1e-3

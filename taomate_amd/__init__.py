@@ -13,6 +13,9 @@ The public names mirror the reference's drop-in surface:
   modules hold them, and replaces the wrapper's ``init_kv_cache()``
 * ``retain_streaming_context``, ``cache_segments``, ``attach_segments``
   (taomate/inference/cache.py), ``compute_av_blocks`` (mask_builder.py:102)
+* ``StreamingGenerator`` (the window and block loop of taomate/inference/model.py:33-248 and
+  model_runtime.py:772-1342: 3-step denoise over the cached context, clean commit, memory
+  update, retention)
 * ``LearnedMemoryState``, ``StreamingMemory`` (taomate/runtime_support/learned_memory.py,
   taomate/inference/memory.py)
 * ``load_generator`` / ``save_generator`` (taomate/inference/model_runtime.py:182-425) and the
@@ -30,6 +33,7 @@ from .cache import (attach_segments, cache_segments, prune_clean_kv_to_sink_rece
 from .kv_cache import (ArenaSpec, KVArena, KVArenaFull, KVCache, KVSpanView, LayerKVCache,
                        _cat_cache, attach_arena, attach_block_arenas, init_kv_cache)
 from .integration import ArenaPlan, Installation, init_kv_cache_for, install
+from .runtime import StreamingGenerator, denoising_sigmas
 from .rope import CausalRopeType, apply_split_rotary_emb, causal_precompute_freqs_cis, generate_freq_grid
 from .streaming import ChunkStream, retain_pinned_recent
 from .memory import LearnedMemoryState, StreamingMemory
@@ -46,5 +50,5 @@ __all__ = [
     "causal_precompute_freqs_cis", "generate_freq_grid", "ChunkStream", "retain_pinned_recent",
     "LearnedMemoryState", "StreamingMemory", "load_generator", "save_generator", "build_prefix_state_payload",
     "load_prefix_state", "save_prefix_state", "attach_arena", "attach_block_arenas", "ArenaPlan",
-    "Installation", "init_kv_cache_for", "install",
+    "Installation", "init_kv_cache_for", "install", "StreamingGenerator", "denoising_sigmas",
 ]

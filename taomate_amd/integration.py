@@ -90,13 +90,17 @@ class ArenaPlan:
     video_frame_tokens: int = 1
 
     @classmethod
-    def for_stream(cls, video_hw: Tuple[int, int], max_video_frames: int = 25, max_audio_tokens: int = 256,
+    def for_stream(cls, video_hw: Tuple[int, int], max_video_frames: int = 32, max_audio_tokens: int = 512,
                    kv_dtype: str = "bf16") -> "ArenaPlan":
-        """Capacities for a stream of ``video_hw`` latent frames.  The defaults
-        cover the reference runtime's largest cache: the first window's 16
+        """Capacities for a stream of ``video_hw`` latent frames.  A slot is
+        busy while any cache view covers it, so the plan must hold everything
+        the caller keeps alive at once.  The defaults cover the reference
+        runtime at the start of the second window: the first window's 16
         frames (blocks of 4, 3, 3, 3, 3 frames appended without pruning,
-        model_runtime.py:1257-1342) and 126 audio tokens, plus the chunk in
-        flight and first-fit slack."""
+        model_runtime.py:1257-1342) still referenced by the caller, the
+        retained sink + 2 recent blocks of the new window, the block in flight
+        and its commit (25 frames), with slack; audio blocks of 25-26 tokens
+        each take 32 slots (appends start on 8-slot boundaries)."""
         hw = int(video_hw[0]) * int(video_hw[1])
         return cls(hw * int(max_video_frames), int(max_audio_tokens), kv_dtype, hw)
 

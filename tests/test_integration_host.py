@@ -76,9 +76,9 @@ def test_install_rebinds_every_site_and_uninstall_restores():
     assert all(isinstance(l, T.LayerKVCache) and l.video_self_k is None and l.a2v_v is None
                for l in cache.layers)
     blk = model.transformer_blocks[1]
-    assert blk.attn1._ltx_arena_plan == T.ArenaSpec(9600, 32, 128, "bf16", 1)
-    assert blk.video_to_audio_attn._ltx_arena_plan == T.ArenaSpec(9600, 32, 64, "bf16", 1)
-    assert blk.audio_attn1._ltx_arena_plan == T.ArenaSpec(256, 32, 64, "bf16", 1)
+    assert blk.attn1._ltx_arena_plan == T.ArenaSpec(12288, 32, 128, "bf16", 1)
+    assert blk.video_to_audio_attn._ltx_arena_plan == T.ArenaSpec(12288, 32, 64, "bf16", 1)
+    assert blk.audio_attn1._ltx_arena_plan == T.ArenaSpec(512, 32, 64, "bf16", 1)
     assert blk.audio_to_video_attn._ltx_arena_name == "layer1.a2v"
     inst.uninstall()
     for name, attr, _ in I.BINDINGS:

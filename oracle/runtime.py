@@ -185,3 +185,26 @@ class StreamOracle:
             self.layers = layers
             out.append((blk, v, a))
         return out
+
+    def rebuild_for_prompt(self, segments, cond, prefix_video, prefix_audio, next_frames: int):
+        """_refresh_conditioning_cache (taomate/inference/runtime.py:386-470):
+        the retained segments' latents (cache order) re-run at sigma 0 under
+        ``cond`` at their global block positions, from an empty cache.
+        Returns the rebuilt layers (the caller keeps their audio self, A2V and
+        V2A fields)."""
+        total = prefix_video.shape[1] + next_frames
+        prefix_blocks = [b for b in compute_blocks(total) if b[2] <= prefix_video.shape[1]]
+        has_sink = segments[0]["block_idx"] == 0
+        warm = len(segments) - int(has_sink)
+        cands = prefix_blocks[1:] if has_sink else prefix_blocks
+        selected = ([prefix_blocks[0]] if has_sink else []) + (cands[-warm:] if warm else [])
+        assert len(selected) == len(segments)
+        layers = None
+        for lb, seg in zip(selected, segments):
+            k = int(seg["block_idx"])
+            gb = compute_blocks(4 + k * 3)[k]
+            video = prefix_video[:, lb[1]:lb[2]]
+            audio = prefix_audio[:, lb[3]:lb[4]]
+            B = video.shape[0]
+            _, _, layers = self._forward(gb, video, audio, torch.zeros(B), self._cond(cond), layers)
+        return layers

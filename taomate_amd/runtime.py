@@ -16,6 +16,11 @@ Host mirror of:
                                   pruning
   generate_next_window            model.py:166-248: per block, denoise, commit,
                                   memory update, retain (sink + 2 recent)
+  _refresh_conditioning_cache     taomate/inference/runtime.py:386-470: on a
+                                  prompt change, the retained blocks re-run at
+                                  sigma 0 under the new conditioning at their
+                                  global positions; their audio self, A2V and
+                                  V2A K/V replace the cache's, video self stays
 
 Every attention, norm and cache kernel runs through ``AVModel.forward_chunk``
 on this package's HIP library; the loop itself only moves latents and cache
@@ -31,7 +36,7 @@ from typing import Any, Callable, Dict, List, Optional, Sequence, Tuple
 
 import torch
 
-from .blocks import AVBlock, compute_av_blocks
+from .blocks import AVBlock, compute_aligned_audio_frames, compute_av_blocks, global_block_at_index
 from .cache import attach_segments, cache_segments, retain_streaming_context
 from .kv_cache import KVCache, LayerKVCache
 from .rope import causal_precompute_freqs_cis
@@ -366,3 +371,51 @@ class StreamingGenerator:
             ao += block.audio_frames
         self.last_cache = cache
         return video, audio
+
+    @torch.no_grad()
+    def refresh_conditioning_cache(self, cache: KVCache, cond: Dict[str, Any], prefix_video: torch.Tensor,
+                                   prefix_audio: torch.Tensor, next_video_shape: Tuple[int, ...],
+                                   memory=None) -> KVCache:
+        """_refresh_conditioning_cache (taomate/inference/runtime.py:386-470).
+
+        ``prefix_video`` [B, F, C, H, W] / ``prefix_audio`` [B, Fa, C] are the
+        retained blocks' latents in cache order (sink block, then the recent
+        blocks).  Each cached segment's latents go through the sigma-0
+        cache-only pass with the new ``cond`` at the segment's global block
+        positions, building a fresh cache; the retained layers then take that
+        cache's audio self, A2V and V2A K/V, while their video self K/V stay
+        as they are (pinned).  The layers are updated in place, as in the
+        reference, and ``cache`` is returned with its segments."""
+        segments = cache_segments(cache)
+        if not segments:
+            raise RuntimeError("The retained cache has no block metadata.")
+        if prefix_audio is None or int(prefix_audio.shape[1]) != compute_aligned_audio_frames(
+                int(prefix_video.shape[1]), FRAMES_PER_BLOCK, FIRST_BLOCK_FRAMES):
+            raise RuntimeError(f"Prefix alignment mismatch: {prefix_video.shape[1]} video frames, "
+                               f"{None if prefix_audio is None else prefix_audio.shape[1]} audio frames.")
+        total = int(prefix_video.shape[1]) + int(next_video_shape[1])
+        local = compute_av_blocks(total, FRAMES_PER_BLOCK, FIRST_BLOCK_FRAMES)
+        prefix_blocks = [b for b in local if b.video_end <= prefix_video.shape[1]]
+        has_sink = int(segments[0]["block_idx"]) == 0
+        warm = len(segments) - int(has_sink)
+        candidates = prefix_blocks[1:] if has_sink else prefix_blocks
+        selected = ([prefix_blocks[0]] if has_sink else []) + (candidates[-warm:] if warm else [])
+        if len(selected) != len(segments):
+            raise RuntimeError("The retained latent prefix does not match the cache layout.")
+        dev = cond["video_context"].device
+        dtype = self.model.patchify_proj.weight.dtype
+        rebuilt = self.init_kv_cache()
+        for lb, seg in zip(selected, segments):
+            gb = global_block_at_index(int(seg["block_idx"]), FRAMES_PER_BLOCK, FIRST_BLOCK_FRAMES)
+            video = prefix_video[:, lb.video_start:lb.video_end].to(device=dev, dtype=dtype)
+            audio = prefix_audio[:, lb.audio_start:lb.audio_end].to(device=dev, dtype=dtype)
+            bc = self._with_memory(memory, cond, dev, dtype)
+            z = torch.zeros(video.shape[0], device=dev, dtype=torch.float32)
+            self.forward(gb, video, audio, z, z, bc, rebuilt, kv_cache_only=True)
+        if len(rebuilt.layers) != len(cache.layers):
+            raise RuntimeError("Conditioning cache refresh failed.")
+        for kept, new in zip(cache.layers, rebuilt.layers):
+            kept.audio_self_k, kept.audio_self_v = new.audio_self_k, new.audio_self_v
+            kept.a2v_k, kept.a2v_v = new.a2v_k, new.a2v_v
+            kept.v2a_k, kept.v2a_v = new.v2a_k, new.v2a_v
+        return attach_segments(cache, segments)

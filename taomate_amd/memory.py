@@ -1,187 +1,395 @@
-"""Learned long-memory state: the detached summaries of generated latents that
-condition later chunks through the blocks' memory adapters.
+"""Learned long memory: detached summaries of the generated latents that
+condition later chunks through the blocks' memory adapters (``taomate_amd.dit``).
 
-Host-side PyTorch on small tensors (a chunk's latents are [B, F, 128, H, W]
-with H x W = 16 x 24 at 512 x 768; the memory is 48 video tokens and 64 audio
-tokens of 128 channels), run on the latents' device.  The adapters that read
-the memory inside the blocks are in ``taomate_amd.dit``.
+Design.  The memory is a value: ``MemoryState``, a frozen record of three
+tracks (video tokens, audio tokens, colour statistics), each an evolving
+summary beside the frozen anchor it is tethered to.  Every operation is a pure
+function from (settings, state, chunk) to a new state.  The decisions are
+tensor arithmetic on the latents' device:
+* the drift gate's sigmoid;
+* the colour-drift threshold;
+* the first-chunk initialisation.
 
-Behaviour follows taomate/runtime_support/learned_memory.py:
-  video / audio token summaries         :192-229
-  EMA update with an anchor tether      :231-249
-  drift gate (pooled cosine, sigmoid)   :120-166, :414-428
-  colour memory (channel statistics,
-  low-frequency prototype, correction)  :35-103, :169-189, :430-487
-  LearnedMemoryState / update /
-  with_conditional_memory               :252-591
-and the production settings of taomate/inference/memory.py:4-29
-(``StreamingMemory``).
+Folding a chunk in therefore queues a few small kernels and never waits for
+the GPU. The reference reads those values back as Python floats. Here they are
+read only by the diagnostic properties. ``LearnedMemoryState`` is the mutable
+handle the runtime holds. It carries the reference's class name, settings
+fields and defaults, and methods (``set_reference``, ``update``,
+``apply_color_memory``, ``with_conditional_memory``).
+
+Behaviour follows taomate/runtime_support/learned_memory.py: token summaries
+:192-229, EMA with an anchor tether :231-249, drift gate :120-166 and
+:414-428, colour memory :35-103, :169-189, :430-487, the state's update order
+:252-591, with the streaming settings of taomate/inference/memory.py:4-29.
 """
 from __future__ import annotations
 
-import math
+import dataclasses
 from dataclasses import dataclass, field
 from typing import Any, Dict, Optional, Tuple
 
 import torch
 import torch.nn.functional as F
 
-__all__ = ["LearnedMemoryState", "StreamingMemory", "summarize_video_memory", "summarize_audio_memory",
-           "apply_color_memory_snapshot"]
+__all__ = ["LearnedMemoryState", "StreamingMemory", "MemoryState", "summarize_video_memory",
+           "summarize_audio_memory", "apply_color_memory_snapshot"]
+
+Tensor = torch.Tensor
 
 
-def _unit(x: float) -> float:
-    """Clamp to [0, 1]."""
-    return min(1.0, max(0.0, float(x)))
+# ---------------------------------------------------------------------------
+# summaries of one chunk
+# ---------------------------------------------------------------------------
+
+def _zscore(x: Tensor, dims: Tuple[int, ...], eps: float) -> Tensor:
+    """Zero mean, unit population std over ``dims`` (std floored at eps)."""
+    centred = x - x.mean(dim=dims, keepdim=True)
+    return centred / x.std(dim=dims, keepdim=True, unbiased=False).clamp_min(eps)
 
 
-def _standardize(x: torch.Tensor, dims: Tuple[int, ...], eps: float) -> torch.Tensor:
-    """(x - mean) / max(std, eps) over ``dims`` (population std)."""
-    mu = x.mean(dim=dims, keepdim=True)
-    sd = x.std(dim=dims, keepdim=True, unbiased=False).clamp_min(eps)
-    return (x - mu) / sd
-
-
-def summarize_video_memory(video_latent: Optional[torch.Tensor], *, downsample: int = 4,
-                           eps: float = 1e-6) -> Optional[torch.Tensor]:
-    """[B, F, C, H, W] latents -> [B, (H/d)(W/d), C] tokens: the frame mean,
-    standardised over the spatial grid per channel, average-pooled by d."""
+def summarize_video_memory(video_latent: Optional[Tensor], *, downsample: int = 4,
+                           eps: float = 1e-6) -> Optional[Tensor]:
+    """[B, F, C, H, W] -> [B, (H/d)(W/d), C]: the chunk's mean frame, z-scored
+    per channel over the spatial grid, average-pooled by d."""
     if video_latent is None or video_latent.numel() == 0:
         return None
     if video_latent.dim() != 5:
         raise ValueError(f"video_latent must be [B,F,C,H,W], got {tuple(video_latent.shape)}")
-    x = _standardize(video_latent.detach().float().mean(dim=1), (-2, -1), eps)
+    frame = _zscore(video_latent.detach().float().mean(dim=1), (2, 3), eps)
     d = max(1, int(downsample))
-    gh, gw = max(1, x.shape[-2] // d), max(1, x.shape[-1] // d)
-    x = F.adaptive_avg_pool2d(x, (gh, gw))
-    B, C = x.shape[:2]
-    return x.flatten(2).transpose(1, 2).contiguous().view(B, gh * gw, C)
+    grid = (max(1, frame.shape[2] // d), max(1, frame.shape[3] // d))
+    return F.adaptive_avg_pool2d(frame, grid).flatten(2).transpose(1, 2).contiguous()
 
 
-def summarize_audio_memory(audio_latent: Optional[torch.Tensor], *, num_tokens: int = 64,
-                           eps: float = 1e-6) -> Optional[torch.Tensor]:
-    """[B, F, C] latents -> [B, num_tokens, C]: standardised over time per
-    channel, average-pooled to ``num_tokens`` steps."""
+def summarize_audio_memory(audio_latent: Optional[Tensor], *, num_tokens: int = 64,
+                           eps: float = 1e-6) -> Optional[Tensor]:
+    """[B, F, C] -> [B, num_tokens, C]: z-scored per channel over time,
+    average-pooled to ``num_tokens`` steps."""
     if audio_latent is None or audio_latent.numel() == 0:
         return None
     if audio_latent.dim() != 3:
         raise ValueError(f"audio_latent must be [B,F,C], got {tuple(audio_latent.shape)}")
-    x = _standardize(audio_latent.detach().float().transpose(1, 2), (-1,), eps)
-    return F.adaptive_avg_pool1d(x, max(1, int(num_tokens))).transpose(1, 2).contiguous()
+    seq = _zscore(audio_latent.detach().float().transpose(1, 2), (2,), eps)
+    return F.adaptive_avg_pool1d(seq, max(1, int(num_tokens))).transpose(1, 2).contiguous()
 
 
-def _channel_stats(latent: torch.Tensor, eps: float) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Per (batch, channel) mean and population std over frames and pixels."""
-    x = latent.detach().float()
-    return x.mean(dim=(1, 3, 4)), x.std(dim=(1, 3, 4), unbiased=False).clamp_min(eps)
-
-
-def _lowfreq_proto(latent: torch.Tensor, grid: int) -> torch.Tensor:
-    """[B, C, g, g]: the frame mean average-pooled to a g x g grid."""
+def color_summary(video_latent: Tensor, grid: int, eps: float) -> Tuple[Tensor, Tensor, Tensor]:
+    """(channel mean [B, C], channel population std [B, C], low-frequency
+    prototype [B, C, g, g]) of a [B, F, C, H, W] chunk."""
+    x = video_latent.detach().float()
     g = max(1, int(grid))
-    return F.adaptive_avg_pool2d(latent.detach().float().mean(dim=1), (g, g))
+    return (x.mean(dim=(1, 3, 4)), x.std(dim=(1, 3, 4), unbiased=False).clamp_min(eps),
+            F.adaptive_avg_pool2d(x.mean(dim=1), (g, g)))
 
 
-def _renorm_channels(latent: torch.Tensor, ref: Tuple[torch.Tensor, torch.Tensor], alpha: float,
-                     eps: float) -> torch.Tensor:
-    """Blend ``alpha`` of the latents moved to the reference channel statistics."""
-    alpha = _unit(alpha)
-    if alpha <= 0.0:
-        return latent
-    mu, sd = _channel_stats(latent, eps)
-    rmu = ref[0].to(device=latent.device, dtype=torch.float32)
-    rsd = ref[1].to(device=latent.device, dtype=torch.float32).clamp_min(eps)
-    bc = lambda t: t[:, None, :, None, None]
+# ---------------------------------------------------------------------------
+# state
+# ---------------------------------------------------------------------------
+
+@dataclass(frozen=True)
+class Track:
+    """An evolving summary and the anchor it is tethered to."""
+    value: Optional[Tensor] = None
+    anchor: Optional[Tensor] = None
+
+
+@dataclass(frozen=True)
+class ColorTrack:
+    """Evolving and anchor colour statistics and low-frequency prototypes,
+    with the last chunk's drift score and whether it was folded in (0-dim
+    device tensors)."""
+    mean: Optional[Tensor] = None
+    std: Optional[Tensor] = None
+    proto: Optional[Tensor] = None
+    anchor_mean: Optional[Tensor] = None
+    anchor_std: Optional[Tensor] = None
+    anchor_proto: Optional[Tensor] = None
+    drift: Optional[Tensor] = None
+    updated: Optional[Tensor] = None
+
+
+@dataclass(frozen=True)
+class MemoryState:
+    video: Track = Track()
+    audio: Track = Track()
+    color: ColorTrack = ColorTrack()
+    referenced: bool = False
+    video_cosine: Optional[Tensor] = None    # last chunk's pooled cosine with the anchor
+    video_gate: Optional[Tensor] = None      # last chunk's update gate
+
+
+# ---------------------------------------------------------------------------
+# pure operations
+# ---------------------------------------------------------------------------
+
+def _u(x):
+    """Clamp to [0, 1] (floats and tensors)."""
+    return x.clamp(0.0, 1.0) if torch.is_tensor(x) else min(1.0, max(0.0, float(x)))
+
+
+def ema_toward(prev: Optional[Tensor], current: Tensor, beta, anchor: Optional[Tensor], tether: float) -> Tensor:
+    """One EMA step of weight ``beta`` toward ``current`` then ``tether`` of
+    the way back to ``anchor``; with no history the current value."""
+    cur = current.detach()
+    if prev is None:
+        return cur.clone()
+    b = _u(beta)
+    out = prev.to(cur) * (1.0 - b) + cur * b
+    t = _u(tether)
+    if anchor is not None and t > 0.0:
+        out = out * (1.0 - t) + anchor.to(cur) * t
+    return out.contiguous()
+
+
+def pooled_cosine(tokens: Tensor, anchor: Tensor, eps: float) -> Tensor:
+    """Batch mean of the cosine between the flattened token grids (their
+    common leading tokens), a 0-dim tensor on the tokens' device."""
+    n = min(tokens.shape[1], anchor.shape[1])
+    a = F.normalize(tokens[:, :n].float().flatten(1), dim=-1, eps=eps)
+    b = F.normalize(anchor[:, :n].to(tokens).float().flatten(1), dim=-1, eps=eps)
+    return (a * b).sum(-1).mean()
+
+
+def soft_gate(score: Tensor, threshold: float, temperature: float, floor: float) -> Tensor:
+    """floor + (1 - floor) sigmoid((score - threshold) / temperature), with
+    the sigmoid taken as exactly 0 or 1 once its argument passes -50 / 50, and
+    a step at the threshold for temperature 0."""
+    lo = _u(floor)
+    if temperature <= 0.0:
+        return torch.where(score >= threshold, torch.ones_like(score), torch.full_like(score, lo))
+    z = (score - threshold) / max(float(temperature), 1e-6)
+    sig = torch.where(z >= 50.0, torch.ones_like(z), torch.where(z <= -50.0, torch.zeros_like(z), torch.sigmoid(z)))
+    return lo + (1.0 - lo) * sig
+
+
+def color_drift(mean: Tensor, std: Tensor, anchor_mean: Tensor, anchor_std: Tensor, eps: float) -> Tensor:
+    """Mean |mean shift| in anchor stds plus 0.1 mean |log std ratio| (0-dim)."""
+    asd = anchor_std.float().clamp_min(eps)
+    shift = ((mean.float() - anchor_mean.float()).abs() / asd).mean()
+    spread = (std.float().clamp_min(eps) / asd).log().abs().mean()
+    return shift + 0.1 * spread
+
+
+def _fold_color(s, col: ColorTrack, video: Tensor, scale) -> ColorTrack:
+    """The chunk's colour statistics folded into the colour track: the first
+    chunk becomes the anchor; later chunks move the statistics by
+    color_update_beta * scale, unless their drift from the anchor passes the
+    threshold, then the tether pulls back toward the anchor."""
+    mean, std, proto = color_summary(video, s.color_proto_grid, s.eps)
+    if col.anchor_mean is None:
+        z = torch.zeros((), device=mean.device)
+        return ColorTrack(mean.clone(), std.clone(), proto.clone(), mean, std, proto, z, torch.ones((), dtype=torch.bool,
+                                                                                                      device=mean.device))
+    drift = color_drift(mean, std, col.anchor_mean, col.anchor_std, s.eps)
+    beta = s.color_update_beta * _u(scale)
+    beta = beta if torch.is_tensor(beta) else torch.tensor(float(beta), device=mean.device)
+    skip = beta <= 0.0
+    if s.color_drift_threshold > 0.0:
+        skip = skip | (drift > s.color_drift_threshold)
+    t = s.color_anchor_tether
+
+    def move(old, new, anc):
+        mixed = old.to(new) * (1.0 - beta) + new * beta
+        if t > 0.0:
+            mixed = mixed * (1.0 - t) + anc.to(new) * t
+        return torch.where(skip, old.to(new), mixed)
+
+    prev_m = col.mean if col.mean is not None else mean
+    prev_s = col.std if col.std is not None else std
+    prev_p = col.proto if col.proto is not None else proto
+    return dataclasses.replace(col, mean=move(prev_m, mean, col.anchor_mean), std=move(prev_s, std, col.anchor_std),
+                               proto=move(prev_p, proto, col.anchor_proto), drift=drift, updated=~skip)
+
+
+def anchored(s, st: MemoryState, video: Optional[Tensor], audio: Optional[Tensor]) -> MemoryState:
+    """The first visible chunk frozen as the anchor of every track (once);
+    an empty track also starts from it."""
+    if not (s.enabled and s.reference_anchor_enabled) or st.referenced:
+        return st
+    v = summarize_video_memory(video, downsample=s.video_downsample, eps=s.eps)
+    a = summarize_audio_memory(audio, num_tokens=s.audio_tokens, eps=s.eps)
+    out = st
+    if v is not None:
+        one = torch.ones((), device=v.device)
+        out = dataclasses.replace(out, video=Track(out.video.value if out.video.value is not None else v.clone(), v),
+                                  video_cosine=one, video_gate=one)
+    if a is not None:
+        out = dataclasses.replace(out, audio=Track(out.audio.value if out.audio.value is not None else a.clone(), a))
+    if s.color_enabled and video is not None and video.numel() > 0:
+        m, sd, p = color_summary(video, s.color_proto_grid, s.eps)
+        c = out.color
+        out = dataclasses.replace(out, color=ColorTrack(
+            c.mean if c.mean is not None else m.clone(), c.std if c.std is not None else sd.clone(),
+            c.proto if c.proto is not None else p.clone(), m, sd, p, torch.zeros((), device=m.device),
+            torch.ones((), dtype=torch.bool, device=m.device)))
+    return dataclasses.replace(out, referenced=v is not None or a is not None)
+
+
+def observe(s, st: MemoryState, video: Optional[Tensor], audio: Optional[Tensor]) -> MemoryState:
+    """One generated chunk folded into the memory: video tokens (EMA gated by
+    the drift from the anchor), audio tokens, then the colour statistics."""
+    if not s.enabled:
+        return st
+    out = st
+    gate = 1.0
+    v = summarize_video_memory(video, downsample=s.video_downsample, eps=s.eps)
+    if v is not None:
+        if out.video.anchor is None:
+            one = torch.ones((), device=v.device)
+            out = dataclasses.replace(out, video=Track(out.video.value, v), video_cosine=one, video_gate=one)
+        elif s.drift_gate_enabled:
+            cos = pooled_cosine(v, out.video.anchor, s.eps)
+            gate = soft_gate(cos, s.drift_gate_threshold, s.drift_gate_temperature, s.drift_gate_min)
+            out = dataclasses.replace(out, video_cosine=cos, video_gate=gate)
+        else:
+            out = dataclasses.replace(out, video_cosine=None, video_gate=torch.ones((), device=v.device))
+        out = dataclasses.replace(out, video=Track(
+            ema_toward(out.video.value, v, s.video_beta * gate, out.video.anchor, s.video_anchor_tether),
+            out.video.anchor))
+    a = summarize_audio_memory(audio, num_tokens=s.audio_tokens, eps=s.eps)
+    if a is not None:
+        anchor = out.audio.anchor if out.audio.anchor is not None else a
+        out = dataclasses.replace(out, audio=Track(
+            ema_toward(out.audio.value, a, s.audio_beta, anchor, s.audio_anchor_tether), anchor))
+    if s.color_enabled and video is not None and video.numel() > 0:
+        out = dataclasses.replace(out, color=_fold_color(s, out.color, video,
+                                                         gate if s.drift_gate_apply_to_color else 1.0))
+    return out
+
+
+def conditioning(s, st: MemoryState) -> Dict[str, Tensor]:
+    """learned_memory_video ([identity anchor |] evolving tokens),
+    learned_memory_audio and learned_memory_color ([mean, log std, anchor
+    mean, anchor log std]) of the state; empty when there is nothing."""
+    out: Dict[str, Tensor] = {}
+    parts = []
+    if s.identity_anchor_enabled and st.video.anchor is not None:
+        parts.append(st.video.anchor * s.identity_anchor_scale if s.identity_anchor_scale != 1.0
+                     else st.video.anchor)
+    if st.video.value is not None:
+        parts.append(st.video.value)
+    if parts:
+        out["learned_memory_video"] = torch.cat(parts, dim=1) if len(parts) > 1 else parts[0]
+    if st.audio.value is not None:
+        out["learned_memory_audio"] = st.audio.value
+    c = st.color
+    if s.color_film_enabled and c.mean is not None:
+        am = c.anchor_mean if c.anchor_mean is not None else c.mean
+        asd = c.anchor_std if c.anchor_std is not None else c.std
+        out["learned_memory_color"] = torch.cat([c.mean, c.std.clamp_min(s.eps).log(), am.to(c.mean),
+                                                 asd.to(c.std).clamp_min(s.eps).log()], dim=-1)
+    return out
+
+
+def _to_reference_stats(latent: Tensor, mean: Tensor, std: Tensor, alpha: float, eps: float) -> Tensor:
+    """``alpha`` of the latents moved onto the given per-channel statistics."""
+    cm, cs, _ = color_summary(latent, 1, eps)
+    shape = (latent.shape[0], 1, latent.shape[2], 1, 1)
     x = latent.float()
-    moved = (x - bc(mu)) / bc(sd).clamp_min(eps) * bc(rsd) + bc(rmu)
-    return (x * (1.0 - alpha) + moved * alpha).to(latent.dtype)
+    target = (x - cm.view(shape)) / cs.view(shape) * std.to(x).clamp_min(eps).view(shape) + mean.to(x).view(shape)
+    return torch.lerp(x, target, alpha).to(latent.dtype)
 
 
-def _pull_lowfreq(latent: torch.Tensor, proto: Optional[torch.Tensor], alpha: float, max_correction: float,
-                  eps: float) -> torch.Tensor:
-    """Add ``alpha`` of the (clamped, bilinearly upsampled) difference between
-    a target low-frequency prototype and the latents' own."""
-    alpha = _unit(alpha)
-    if alpha <= 0.0 or proto is None:
-        return latent
-    delta = proto.to(device=latent.device, dtype=torch.float32) - _lowfreq_proto(latent, int(proto.shape[-1]))
+def _toward_prototype(latent: Tensor, proto: Tensor, alpha: float, max_correction: float, eps: float) -> Tensor:
+    """Add ``alpha`` of the prototype difference (clamped per channel to
+    max_correction batch-mean stds, upsampled bilinearly) to every frame."""
+    _, cs, own = color_summary(latent, proto.shape[-1], eps)
+    delta = proto.to(own) - own
     if max_correction > 0.0:
-        lim = _channel_stats(latent, eps)[1].float().mean(dim=0).view(1, -1, 1, 1) * float(max_correction)
-        delta = torch.maximum(torch.minimum(delta, lim), -lim)
+        lim = (cs.mean(dim=0) * float(max_correction)).view(1, -1, 1, 1)
+        delta = torch.clamp(delta, -lim, lim)
     delta = F.interpolate(delta, size=tuple(latent.shape[-2:]), mode="bilinear", align_corners=False)
-    return (latent.float() + alpha * delta[:, None]).to(latent.dtype)
+    return (latent.float() + alpha * delta.unsqueeze(1)).to(latent.dtype)
 
 
-def apply_color_memory_snapshot(video_latent: Optional[torch.Tensor],
-                                snapshot: Optional[Dict[str, Any]]) -> Optional[torch.Tensor]:
-    """Colour correction of generated latents from a memory snapshot
-    (channel statistics, then the low-frequency prototype)."""
+def color_corrected(s, st: MemoryState, video: Optional[Tensor]) -> Optional[Tensor]:
+    """The chunk's colours pulled toward the colour memory: channel
+    statistics (color_alpha), then the low-frequency prototype
+    (color_proto_alpha, limited by color_max_correction)."""
+    c = st.color
+    if video is None or not s.color_enabled or c.mean is None or (s.color_alpha <= 0.0 and s.color_proto_alpha <= 0.0):
+        return video
+    out = video
+    if s.color_alpha > 0.0:
+        out = _to_reference_stats(out, c.mean, c.std, s.color_alpha, s.eps)
+    if s.color_proto_alpha > 0.0 and c.proto is not None:
+        out = _toward_prototype(out, c.proto, s.color_proto_alpha, s.color_max_correction, s.eps)
+    return out
+
+
+def apply_color_memory_snapshot(video_latent: Optional[Tensor],
+                                snapshot: Optional[Dict[str, Any]]) -> Optional[Tensor]:
+    """Colour correction from a detached snapshot (``LearnedMemoryState.color_snapshot``)."""
     if video_latent is None or not snapshot:
         return video_latent
     eps = float(snapshot.get("eps", 1e-6))
     out = video_latent
-    if float(snapshot.get("color_alpha", 0.0)) > 0.0 and snapshot.get("color_stats") is not None:
-        out = _renorm_channels(out, snapshot["color_stats"], float(snapshot["color_alpha"]), eps)
-    if float(snapshot.get("color_proto_alpha", 0.0)) > 0.0:
-        out = _pull_lowfreq(out, snapshot.get("color_proto"), float(snapshot["color_proto_alpha"]),
-                            float(snapshot.get("color_max_correction", 0.5)), eps)
+    stats = snapshot.get("color_stats")
+    if float(snapshot.get("color_alpha", 0.0)) > 0.0 and stats is not None:
+        out = _to_reference_stats(out, stats[0], stats[1], _u(snapshot["color_alpha"]), eps)
+    if float(snapshot.get("color_proto_alpha", 0.0)) > 0.0 and snapshot.get("color_proto") is not None:
+        out = _toward_prototype(out, snapshot["color_proto"], _u(snapshot["color_proto_alpha"]),
+                                float(snapshot.get("color_max_correction", 0.5)), eps)
     return out
 
 
-def _stats_drift(stats, anchor, eps: float) -> float:
-    """Mean |Δmean| / anchor std plus 0.1 x mean |log(std ratio)|."""
-    mu, sd = stats
-    amu, asd = anchor[0].to(mu.device).float(), anchor[1].to(sd.device).float().clamp_min(eps)
-    mean_term = ((mu.float() - amu).abs() / asd).mean()
-    std_term = torch.log(sd.float().clamp_min(eps) / asd).abs().mean()
-    return float((mean_term + 0.1 * std_term).detach().cpu())
+# ---------------------------------------------------------------------------
+# the mutable handle
+# ---------------------------------------------------------------------------
+
+def _state_attr(path: str, doc: str):
+    """A read/write attribute of the handle that lives inside the frozen state."""
+    head, _, tail = path.partition(".")
+
+    def get(self):
+        v = getattr(self.state, head)
+        return getattr(v, tail) if tail else v
+
+    def put(self, value):
+        if tail:
+            part = dataclasses.replace(getattr(self.state, head), **{tail: value})
+            self.state = dataclasses.replace(self.state, **{head: part})
+        else:
+            self.state = dataclasses.replace(self.state, **{head: value})
+    return property(get, put, doc=doc)
 
 
-def _token_cosine(current: torch.Tensor, anchor: torch.Tensor, eps: float) -> float:
-    """Mean over the batch of the cosine between the flattened token grids
-    (the common leading tokens when the counts differ)."""
-    cur = current.detach().float()
-    anc = anchor.detach().to(device=cur.device, dtype=torch.float32)
-    if cur.dim() != 3 or anc.dim() != 3:
-        return 1.0
-    n = min(cur.shape[1], anc.shape[1])
-    if n <= 0:
-        return 1.0
-    a = F.normalize(cur[:, :n].flatten(1), dim=-1, eps=eps)
-    b = F.normalize(anc[:, :n].flatten(1), dim=-1, eps=eps)
-    return float((a * b).sum(-1).mean().detach().cpu())
+def _pair_attr(head: str, first: str, second: str, doc: str):
+    def get(self):
+        c = getattr(self.state, head)
+        a, b = getattr(c, first), getattr(c, second)
+        return None if a is None else (a, b)
+
+    def put(self, value):
+        a, b = (None, None) if value is None else value
+        part = dataclasses.replace(getattr(self.state, head), **{first: a, second: b})
+        self.state = dataclasses.replace(self.state, **{head: part})
+    return property(get, put, doc=doc)
 
 
-def _gate(score: float, threshold: float, temperature: float, floor: float) -> float:
-    """floor + (1 - floor) * sigmoid((score - threshold) / temperature); a
-    step at the threshold when the temperature is 0."""
-    floor = _unit(floor)
-    if temperature <= 0.0:
-        return 1.0 if score >= threshold else floor
-    z = (float(score) - float(threshold)) / max(float(temperature), 1e-6)
-    s = 1.0 if z >= 50.0 else 0.0 if z <= -50.0 else 1.0 / (1.0 + math.exp(-z))
-    return floor + (1.0 - floor) * s
+def _scalar_attr(path: str, as_bool: bool, doc: str):
+    """A diagnostic scalar: the device tensor read back on access."""
+    inner = _state_attr(path, doc)
 
+    def get(self):
+        v = inner.fget(self)
+        if v is None:
+            return None
+        return bool(v) if as_bool else float(v)
 
-def _blend(prev: Optional[torch.Tensor], anchor: Optional[torch.Tensor], cur: torch.Tensor, beta: float,
-           tether: float) -> torch.Tensor:
-    """EMA step prev (1 - beta) + cur beta, then pulled ``tether`` of the way
-    back to the anchor; the first step takes the current tokens."""
-    cur = cur.detach().contiguous()
-    if prev is None:
-        return cur.clone()
-    beta, tether = _unit(beta), _unit(tether)
-    out = prev.detach().to(device=cur.device, dtype=cur.dtype) * (1.0 - beta) + cur * beta
-    if anchor is not None and tether > 0.0:
-        out = out * (1.0 - tether) + anchor.detach().to(device=cur.device, dtype=cur.dtype) * tether
-    return out.detach().contiguous()
+    def put(self, value):
+        if value is None:
+            inner.fset(self, None)
+        else:
+            inner.fset(self, torch.tensor(bool(value) if as_bool else float(value)))
+    return property(get, put, doc=doc)
 
 
 @dataclass
 class LearnedMemoryState:
-    """EMA memory of generated chunks (video tokens, audio tokens, colour
-    statistics) with a frozen first-chunk anchor; field names and defaults
-    of learned_memory.py:252-277."""
+    """The memory handle with the reference's settings fields and defaults
+    (learned_memory.py:252-277); the state itself is ``state``, a
+    ``MemoryState`` replaced by every update."""
     enabled: bool = False
     video_downsample: int = 4
     audio_tokens: int = 64
@@ -207,25 +415,12 @@ class LearnedMemoryState:
     color_film_enabled: bool = False
     reference_anchor_enabled: bool = False
     eps: float = 1e-6
-    # evolving state
-    video: Optional[torch.Tensor] = field(default=None, init=False, repr=False)
-    audio: Optional[torch.Tensor] = field(default=None, init=False, repr=False)
-    video_anchor: Optional[torch.Tensor] = field(default=None, init=False, repr=False)
-    audio_anchor: Optional[torch.Tensor] = field(default=None, init=False, repr=False)
-    color_stats: Optional[Tuple[torch.Tensor, torch.Tensor]] = field(default=None, init=False, repr=False)
-    color_anchor_stats: Optional[Tuple[torch.Tensor, torch.Tensor]] = field(default=None, init=False, repr=False)
-    color_proto: Optional[torch.Tensor] = field(default=None, init=False, repr=False)
-    color_anchor_proto: Optional[torch.Tensor] = field(default=None, init=False, repr=False)
-    color_last_drift: Optional[float] = field(default=None, init=False)
-    color_last_updated: bool = field(default=False, init=False)
-    video_last_anchor_cosine: Optional[float] = field(default=None, init=False)
-    video_last_update_gate: Optional[float] = field(default=None, init=False)
-    reference_initialized: bool = field(default=False, init=False)
+    state: MemoryState = field(default_factory=MemoryState, init=False, repr=False)
 
     def __post_init__(self) -> None:
         for name in ("video_beta", "audio_beta", "video_anchor_tether", "audio_anchor_tether", "drift_gate_min",
                      "color_alpha", "color_proto_alpha", "color_update_beta", "color_anchor_tether"):
-            setattr(self, name, _unit(getattr(self, name)))
+            setattr(self, name, _u(getattr(self, name)))
         self.video_downsample = max(1, int(self.video_downsample))
         self.audio_tokens = max(1, int(self.audio_tokens))
         self.color_proto_grid = max(1, int(self.color_proto_grid))
@@ -234,162 +429,56 @@ class LearnedMemoryState:
         self.color_max_correction = max(0.0, float(self.color_max_correction))
         self.color_enabled = bool(self.color_enabled or self.color_film_enabled)
 
+    # the state under the reference's attribute names (the prefix-state file uses them)
+    video = _state_attr("video.value", "evolving video tokens [B, N, C]")
+    audio = _state_attr("audio.value", "evolving audio tokens [B, T, C]")
+    video_anchor = _state_attr("video.anchor", "anchor video tokens")
+    audio_anchor = _state_attr("audio.anchor", "anchor audio tokens")
+    color_proto = _state_attr("color.proto", "evolving low-frequency prototype [B, C, g, g]")
+    color_anchor_proto = _state_attr("color.anchor_proto", "anchor prototype")
+    color_stats = _pair_attr("color", "mean", "std", "evolving (channel mean, channel std)")
+    color_anchor_stats = _pair_attr("color", "anchor_mean", "anchor_std", "anchor (channel mean, channel std)")
+    reference_initialized = _state_attr("referenced", "whether set_reference took effect")
+    color_last_drift = _scalar_attr("color.drift", False, "last chunk's colour drift from the anchor")
+    color_last_updated = _scalar_attr("color.updated", True, "whether the last chunk moved the colour memory")
+    video_last_anchor_cosine = _scalar_attr("video_cosine", False, "last chunk's pooled cosine with the anchor")
+    video_last_update_gate = _scalar_attr("video_gate", False, "last chunk's drift gate")
+
     def reset(self) -> None:
-        self.video = self.audio = self.video_anchor = self.audio_anchor = None
-        self.color_stats = self.color_anchor_stats = None
-        self.color_proto = self.color_anchor_proto = None
-        self.color_last_drift = self.video_last_anchor_cosine = self.video_last_update_gate = None
-        self.color_last_updated = False
-        self.reference_initialized = False
+        self.state = MemoryState()
 
-    # ---- summaries of one chunk ----
-    def _video_tokens(self, video_latent):
-        return summarize_video_memory(video_latent, downsample=self.video_downsample, eps=self.eps)
+    def set_reference(self, video_latent: Optional[Tensor], audio_latent: Optional[Tensor] = None) -> None:
+        self.state = anchored(self, self.state, video_latent, audio_latent)
 
-    def _audio_tokens(self, audio_latent):
-        return summarize_audio_memory(audio_latent, num_tokens=self.audio_tokens, eps=self.eps)
+    def update(self, video_latent: Optional[Tensor], audio_latent: Optional[Tensor] = None) -> None:
+        self.state = observe(self, self.state, video_latent, audio_latent)
 
-    def _color_of(self, video_latent):
-        stats = tuple(t.detach().contiguous().clone() for t in _channel_stats(video_latent, self.eps))
-        return stats, _lowfreq_proto(video_latent, self.color_proto_grid).detach().contiguous().clone()
-
-    # ---- colour memory ----
     def color_snapshot(self) -> Optional[Dict[str, Any]]:
-        if not self.color_enabled or self.color_stats is None or (
-                self.color_alpha <= 0.0 and self.color_proto_alpha <= 0.0):
+        c = self.state.color
+        if not self.color_enabled or c.mean is None or (self.color_alpha <= 0.0 and self.color_proto_alpha <= 0.0):
             return None
-        return {"color_stats": tuple(t.detach() for t in self.color_stats),
-                "color_proto": None if self.color_proto is None else self.color_proto.detach(),
-                "color_alpha": self.color_alpha, "color_proto_alpha": self.color_proto_alpha,
-                "color_max_correction": self.color_max_correction, "eps": self.eps}
+        return {"color_stats": (c.mean, c.std), "color_proto": c.proto, "color_alpha": self.color_alpha,
+                "color_proto_alpha": self.color_proto_alpha, "color_max_correction": self.color_max_correction,
+                "eps": self.eps}
 
-    def apply_color_memory(self, video_latent: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
-        return apply_color_memory_snapshot(video_latent, self.color_snapshot())
-
-    def _update_color_memory(self, video_latent: Optional[torch.Tensor], *, update_scale: float = 1.0) -> None:
-        if not self.color_enabled or video_latent is None or video_latent.numel() == 0:
-            return
-        stats, proto = self._color_of(video_latent)
-        if self.color_anchor_stats is None:
-            self.color_anchor_stats, self.color_anchor_proto = stats, proto
-            self.color_stats, self.color_proto = tuple(t.clone() for t in stats), proto.clone()
-            self.color_last_drift, self.color_last_updated = 0.0, True
-            return
-        self.color_last_drift = _stats_drift(stats, self.color_anchor_stats, self.eps)
-        beta = self.color_update_beta * _unit(update_scale)
-        if (self.color_drift_threshold > 0.0 and self.color_last_drift > self.color_drift_threshold) or beta <= 0.0:
-            self.color_last_updated = False
-            return
-        tether = self.color_anchor_tether
-        prev = self.color_stats or stats
-        mixed = [(1.0 - beta) * o.to(n.device) + beta * n for o, n in zip(prev, stats)]
-        if tether > 0.0:
-            mixed = [(1.0 - tether) * m + tether * a.to(m.device) for m, a in zip(mixed, self.color_anchor_stats)]
-        self.color_stats = tuple(t.detach().contiguous() for t in mixed)
-        p = (1.0 - beta) * (self.color_proto if self.color_proto is not None else proto).to(proto.device) \
-            + beta * proto
-        if tether > 0.0 and self.color_anchor_proto is not None:
-            p = (1.0 - tether) * p + tether * self.color_anchor_proto.to(proto.device)
-        self.color_proto = p.detach().contiguous()
-        self.color_last_updated = True
-
-    def _color_condition_vector(self) -> Optional[torch.Tensor]:
-        """[B, 4C]: mean, log std, anchor mean, anchor log std."""
-        if not self.color_film_enabled or self.color_stats is None:
-            return None
-        mu, sd = self.color_stats
-        amu, asd = self.color_anchor_stats if self.color_anchor_stats is not None else (mu, sd)
-        return torch.cat([mu.detach(), sd.detach().clamp_min(self.eps).log(), amu.detach().to(mu.device),
-                          asd.detach().to(sd.device).clamp_min(self.eps).log()], dim=-1)
-
-    # ---- anchor, update, conditioning ----
-    def set_reference(self, video_latent: Optional[torch.Tensor], audio_latent: Optional[torch.Tensor] = None):
-        """Freeze the first visible chunk as the anchor (once)."""
-        if not (self.enabled and self.reference_anchor_enabled) or self.reference_initialized:
-            return
-        v = self._video_tokens(video_latent)
-        if v is not None:
-            self.video_anchor = v.detach().contiguous().clone()
-            if self.video is None:
-                self.video = self.video_anchor.clone()
-            self.video_last_anchor_cosine = self.video_last_update_gate = 1.0
-        a = self._audio_tokens(audio_latent)
-        if a is not None:
-            self.audio_anchor = a.detach().contiguous().clone()
-            if self.audio is None:
-                self.audio = self.audio_anchor.clone()
-        if self.color_enabled and video_latent is not None and video_latent.numel() > 0:
-            stats, proto = self._color_of(video_latent)
-            self.color_anchor_stats, self.color_anchor_proto = stats, proto
-            if self.color_stats is None:
-                self.color_stats = tuple(t.clone() for t in stats)
-            if self.color_proto is None:
-                self.color_proto = proto.clone()
-            self.color_last_drift, self.color_last_updated = 0.0, True
-        if v is not None or a is not None:
-            self.reference_initialized = True
-
-    def _video_update_gate(self, tokens: torch.Tensor) -> float:
-        if not self.drift_gate_enabled or self.video_anchor is None:
-            self.video_last_anchor_cosine, self.video_last_update_gate = None, 1.0
-            return 1.0
-        score = _token_cosine(tokens, self.video_anchor, self.eps)
-        g = _gate(score, self.drift_gate_threshold, self.drift_gate_temperature, self.drift_gate_min)
-        self.video_last_anchor_cosine, self.video_last_update_gate = score, g
-        return g
-
-    def update(self, video_latent: Optional[torch.Tensor], audio_latent: Optional[torch.Tensor] = None) -> None:
-        """Fold one generated chunk into the memory."""
-        if not self.enabled:
-            return
-        gate = 1.0
-        v = self._video_tokens(video_latent)
-        if v is not None:
-            if self.video_anchor is None:
-                self.video_anchor = v.detach().contiguous().clone()
-                self.video_last_anchor_cosine = self.video_last_update_gate = 1.0
-            else:
-                gate = self._video_update_gate(v)
-            self.video = _blend(self.video, self.video_anchor, v, self.video_beta * gate, self.video_anchor_tether)
-        a = self._audio_tokens(audio_latent)
-        if a is not None:
-            if self.audio_anchor is None:
-                self.audio_anchor = a.detach().contiguous().clone()
-            self.audio = _blend(self.audio, self.audio_anchor, a, self.audio_beta, self.audio_anchor_tether)
-        self._update_color_memory(video_latent, update_scale=gate if self.drift_gate_apply_to_color else 1.0)
-
-    def _video_condition_memory(self) -> Optional[torch.Tensor]:
-        parts = []
-        if self.identity_anchor_enabled and self.video_anchor is not None:
-            anchor = self.video_anchor.detach()
-            parts.append(anchor * self.identity_anchor_scale if self.identity_anchor_scale != 1.0 else anchor)
-        if self.video is not None:
-            parts.append(self.video)
-        if not parts:
-            return None
-        return parts[0] if len(parts) == 1 else torch.cat(parts, dim=1)
+    def apply_color_memory(self, video_latent: Optional[Tensor]) -> Optional[Tensor]:
+        return color_corrected(self, self.state, video_latent)
 
     def with_conditional_memory(self, conditional_dict: Dict[str, Any], *, device=None,
                                 dtype=None) -> Dict[str, Any]:
-        """``conditional_dict`` plus learned_memory_video / _audio / _color."""
-        vm = self._video_condition_memory()
-        if not self.enabled or (vm is None and self.audio is None):
+        """``conditional_dict`` plus the memory tensors (moved to ``device`` /
+        ``dtype`` when given); unchanged when the memory is off or empty."""
+        mem = conditioning(self, self.state) if self.enabled else {}
+        if "learned_memory_video" not in mem and "learned_memory_audio" not in mem:
             return conditional_dict
-        move = (lambda t: t.to(device=device or t.device, dtype=dtype or t.dtype)) \
-            if (device is not None or dtype is not None) else (lambda t: t)
         out = dict(conditional_dict)
-        if vm is not None:
-            out["learned_memory_video"] = move(vm)
-        if self.audio is not None:
-            out["learned_memory_audio"] = move(self.audio)
-        color = self._color_condition_vector()
-        if color is not None:
-            out["learned_memory_color"] = move(color)
+        for k, v in mem.items():
+            out[k] = v.to(device=device or v.device, dtype=dtype or v.dtype)
         return out
 
 
 class StreamingMemory(LearnedMemoryState):
-    """The production settings (taomate/inference/memory.py:4-29): identity
+    """The streaming settings (taomate/inference/memory.py:4-29): identity
     anchor + EMA video tokens, drift gate, colour memory and FiLM."""
 
     def __init__(self) -> None:

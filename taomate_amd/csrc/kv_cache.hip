@@ -82,9 +82,12 @@ __global__ void __launch_bounds__(kQuantThreads) kv_quant_kernel(
       v[4] = bb.x; v[5] = bb.y; v[6] = bb.z; v[7] = bb.w;
     }
   };
-  auto store8 = [&](int idx, const float (&v)[8], float sc, float r) {
+  auto store8 = [&](int idx, const float (&v)[8], float sc, float r, bool corrected) {
     float q[8];
-    quotients_for_e4m3(v, sc, r, q);
+    if constexpr (sizeof(TS) == 2)
+      quotients_e4m3_bf16(v, sc, r, corrected, q);
+    else
+      quotients_for_e4m3(v, sc, r, q);
     const uint32_t lo = pack4_e4m3(q[0], q[1], q[2], q[3]);
     const uint32_t hi = pack4_e4m3(q[4], q[5], q[6], q[7]);
     const int t = idx / cpr, c = idx % cpr;
@@ -112,7 +115,7 @@ __global__ void __launch_bounds__(kQuantThreads) kv_quant_kernel(
   for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
   constexpr int kWaves = kQuantThreads / 64;
   __shared__ float red[kWaves];
-  __shared__ float scale_s;
+  __shared__ float scale_s, max_s;
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -120,34 +123,38 @@ __global__ void __launch_bounds__(kQuantThreads) kv_quant_kernel(
     for (int w = 1; w < kWaves; ++w) m = fmaxf(m, red[w]);
     const float sc = m > 0.0f ? __fdiv_rn(m, 448.0f) : 1.0f;
     scale_s = sc;
+    max_s = m;
     scales[b * sc_bs + h * sc_hs + f] = sc;
   }
   __syncthreads();
   const float sc = scale_s;
   const float r = __fdiv_rn(1.0f, sc);
+  const bool corrected = max_s >= kCorrectedMinMax;
 #pragma unroll
   for (int i = 0; i < kQuantRegs; ++i) {
     const int idx = threadIdx.x + i * kQuantThreads;
-    if (idx < n) store8(idx, v[i], sc, r);
+    if (idx < n) store8(idx, v[i], sc, r, corrected);
   }
   for (int idx = threadIdx.x + kQuantRegs * kQuantThreads; idx < n; idx += kQuantThreads) {
     float t[8];
     load8(idx, t);
-    store8(idx, t, sc, r);
+    store8(idx, t, sc, r, corrected);
   }
 }
 
 // fp8 quantise of bf16 rows: one 1024-thread workgroup per (frame, h, b,
 // tensor), each thread holding up to kPairRegs raw 16-byte chunks (8 bf16) of
 // its frame between the absmax pass and the quantise pass, so the frame is
-// read from memory once (chunks past kPairRegs * 1024 are read again).  K and
-// V go in one launch (blockIdx.z = b + B * tensor): a 16x24 frame of 32 x 128
-// heads at B = 2 is 384 workgroups, one round at two workgroups per CU.  The
-// arithmetic is that of kv_quant_kernel, so the codes and scales are
-// bit-identical to it.  (Measured: 256-thread workgroups holding 24 chunks
-// each are slower; the per-thread chain of chunks, not occupancy, bounds it.)
+// read from memory once (chunks past kPairRegs * 1024 are read again; a 16x24
+// frame of a 128-wide head is exactly 6 chunks per thread).  K and V go in one
+// launch (blockIdx.z = b + B * tensor): a 16x24 frame of 32 x 128 heads at
+// B = 2 is 384 workgroups, one round at two workgroups per CU (56 VGPRs; the
+// eighth register pair of an earlier version cost the second workgroup).  The
+// quotients are the corrected ones of quotients_e4m3_bf16, the same as
+// kv_quant_kernel's for bf16 sources, so codes and scales are bit-identical
+// to it.
 constexpr int kPairThreads = 1024;
-constexpr int kPairRegs = 8;
+constexpr int kPairRegs = 6;
 
 struct QuantTensor {
   const uint16_t* src;
@@ -183,7 +190,7 @@ __global__ void __launch_bounds__(kPairThreads) kv_quant_pair_kernel(const Quant
       m = fmaxf(m, fmaxf(fabsf(bf16_bits_to_f32(w[i] & 0xFFFFu)), fabsf(bf16_bits_to_f32(w[i] >> 16))));
     return m;
   };
-  auto store = [&](int idx, uint4 r, float sc, float rc) {
+  auto store = [&](int idx, uint4 r, float sc, float rc, bool corrected) {
     const uint32_t w[4] = {r.x, r.y, r.z, r.w};
     float x[8], q[8];
 #pragma unroll
@@ -191,7 +198,7 @@ __global__ void __launch_bounds__(kPairThreads) kv_quant_pair_kernel(const Quant
       x[2 * i] = bf16_bits_to_f32(w[i] & 0xFFFFu);
       x[2 * i + 1] = bf16_bits_to_f32(w[i] >> 16);
     }
-    quotients_for_e4m3(x, sc, rc, q);
+    quotients_e4m3_bf16(x, sc, rc, corrected, q);
     const int t = idx / cpr, c = idx % cpr;
     *reinterpret_cast<uint2*>(dbase + (int64_t)t * a.d_ls + c * 8) =
         make_uint2(pack4_e4m3(q[0], q[1], q[2], q[3]), pack4_e4m3(q[4], q[5], q[6], q[7]));
@@ -224,12 +231,14 @@ __global__ void __launch_bounds__(kPairThreads) kv_quant_pair_kernel(const Quant
   const float sc = m > 0.0f ? __fdiv_rn(m, 448.0f) : 1.0f;
   if (threadIdx.x == 0) T.scales[b * a.sc_bs + h * a.sc_hs + f] = sc;
   const float rc = __fdiv_rn(1.0f, sc);
+  const bool corrected = m >= kCorrectedMinMax;
 #pragma unroll
   for (int i = 0; i < kPairRegs; ++i) {
     const int idx = threadIdx.x + i * kPairThreads;
-    if (idx < n) store(idx, raw[i], sc, rc);
+    if (idx < n) store(idx, raw[i], sc, rc, corrected);
   }
-  for (int idx = threadIdx.x + kPairRegs * kPairThreads; idx < n; idx += kPairThreads) store(idx, load(idx), sc, rc);
+  for (int idx = threadIdx.x + kPairRegs * kPairThreads; idx < n; idx += kPairThreads)
+    store(idx, load(idx), sc, rc, corrected);
 }
 
 inline int launch_quant_pair(const QuantPair& a, int ntensors, int64_t L, int64_t H, hipStream_t st) {

@@ -88,6 +88,39 @@ __device__ __forceinline__ void quotients_for_e4m3(const float (&x)[N], float sc
   }
 }
 
+// Frame maxima m >= kCorrectedMinMax quantise with quotient_e4m3_corrected:
+// for every bf16 maximum m >= 2^-96 and every bf16 value x with |x| <= m, the
+// e4m3 code of quotient_e4m3_corrected(x, sc, fl(1 / sc)), sc = fl(m / 448),
+// equals the code of fl(x / sc) (checked exhaustively over all such pairs by
+// the CPU tests).  Below it (maxima of 2^-96 and less) the division is exact.
+constexpr float kCorrectedMinMax = 0x1p-96f;
+
+// fl(x / sc) up to last bits that cannot change an e4m3 code (see
+// kCorrectedMinMax): q = fl(x * r) for r = fl(1 / sc), the residual x - q * sc
+// in one fused multiply-add, then one correction q + residual * r (Markstein's
+// correction step); the sign is taken from x so that -0 stays -0.  Straight
+// line, one multiply and two FMAs per value.
+__device__ __forceinline__ float quotient_e4m3_corrected(float x, float sc, float r) {
+  const float q = __fmul_rn(x, r);
+  const float e = __fmaf_rn(-q, sc, x);
+  return copysignf(__fmaf_rn(e, r, q), x);
+}
+
+// Quotients of a chunk of bf16-sourced values for e4m3 rounding: the corrected
+// quotient when the frame maximum allows it (a workgroup-uniform choice), the
+// exact division otherwise.
+template <int N>
+__device__ __forceinline__ void quotients_e4m3_bf16(const float (&x)[N], float sc, float r, bool corrected,
+                                                    float (&q)[N]) {
+  if (corrected) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) q[i] = quotient_e4m3_corrected(x[i], sc, r);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) q[i] = __fdiv_rn(x[i], sc);
+  }
+}
+
 // Four float32 values -> four OCP e4m3fn codes (byte i = value i): clamp to
 // +-448, then the gfx950 converter rounds to nearest even.
 __device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d) {

@@ -248,48 +248,58 @@ __device__ __forceinline__ float rnd(float v) {
   else return v;
 }
 
-// Rows handled by one workgroup of the fused kernel (all loads of its rows are
-// issued before the first reduction).  Measured at 1152 rows x 4096, B = 2:
-// 2 rows 17.8 us, 1 row 18.5 us, 4 rows 19.8 us.
+// Rows handled by one workgroup (all loads of its rows are issued before the
+// first reduction).
 constexpr int NR_ROWS = 2;
 
-// Workgroup -> (row group, batch, side).  The combos (batch, side) of one row
-// group share its RoPE-table rows; blocks are dispatched round-robin over the
-// 8 XCDs (block id % 8), so the combos of a row group are given consecutive
-// blocks of the same XCD and read the table from its L2 after the first.
-struct NormWork {
-  int64_t rg;
-  int b, side;
-};
-__device__ __forceinline__ NormWork norm_work(int64_t bid, int ncombo, int B) {
-  const int64_t x = bid & 7, t = bid >> 3;
-  NormWork w;
-  const int combo = (int)(t % ncombo);
-  w.rg = (t / ncombo) * 8 + x;
-  w.b = combo % B;
-  w.side = combo / B;
-  return w;
+// Norm grid: blockIdx = (row group, batch, side 0 = q / 1 = k), gridDim.x a
+// multiple of 8.  Workgroups are dispatched round-robin over the 8 XCDs in
+// linear order, so every (batch, side) of row group x runs on XCD x % 8 and
+// reads the group's RoPE-table rows from that XCD's L2 after the first.  The
+// mapping needs no division: a workgroup lives about one memory round trip,
+// and a scalar divide chain ahead of its first load lengthens every one.
+inline int64_t norm_grid_x(int64_t rows) { return ceil_div(ceil_div(rows, NR_ROWS), 8) * 8; }
+
+// Per-side fields selected with scalar selects (a reference to one of two
+// kernel-argument structs picked at run time makes the compiler reload them).
+__device__ __forceinline__ NormRopeSide pick_side(const NormRopeSide& q, const NormRopeSide& k, bool kside) {
+  NormRopeSide s;
+  s.in = kside ? k.in : q.in;
+  s.out = kside ? k.out : q.out;
+  s.gamma = kside ? k.gamma : q.gamma;
+  s.cos = kside ? k.cos : q.cos;
+  s.sin = kside ? k.sin : q.sin;
+  s.len = kside ? k.len : q.len;
+  s.in_bs = kside ? k.in_bs : q.in_bs;
+  s.in_ls = kside ? k.in_ls : q.in_ls;
+  s.out_bs = kside ? k.out_bs : q.out_bs;
+  s.out_ls = kside ? k.out_ls : q.out_ls;
+  s.tb = kside ? k.tb : q.tb;
+  s.th = kside ? k.th : q.th;
+  s.tt = kside ? k.tt : q.tt;
+  s.eps = kside ? k.eps : q.eps;
+  return s;
 }
 
-// The rows of work item ``bid`` (see norm_work); every thread of the block
-// calls it (one barrier when normalising).
-template <typename T, typename TT>
-__device__ __forceinline__ void norm_rope_rows(const NormRopeSide& qs, const NormRopeSide& ks, int H, int D, int B,
-                                               int nsides, int64_t bid) {
+// The NR_ROWS rows of row group ``rg`` of (batch b, side); every thread of the
+// block calls it (one barrier when normalising).  CPD: D / 16 when known at
+// compile time (8 for D = 128, 4 for D = 64), 0 otherwise.
+template <typename T, typename TT, int CPD>
+__device__ __forceinline__ void norm_rope_rows(const NormRopeSide& qs, const NormRopeSide& ks, int H, int D,
+                                               int64_t rg, int b, int side) {
   constexpr int R = NR_ROWS;
-  const NormWork wk = norm_work(bid, B * nsides, B);
-  const NormRopeSide& sd = (wk.side == 0) ? qs : ks;
-  const int64_t row0 = wk.rg * R;
+  const NormRopeSide sd = pick_side(qs, ks, side != 0);
+  const int64_t row0 = rg * R;
   if (row0 >= sd.len) return;  // uniform across the block
   const int nr = (int)(sd.len - row0 < R ? sd.len - row0 : R);
-  const int b = wk.b;
   const int HD = H * D;
-  const int cpd = D / 16;  // chunks of 8 pairs per head
+  const int cpd = CPD > 0 ? CPD : D / 16;  // chunks of 8 pairs per head
+  const int dh = CPD > 0 ? CPD * 16 : D;
   const int tid = threadIdx.x;
   const int h = tid / cpd;
   const int c = tid % cpd;
-  const int e1 = h * D + c * 8;
-  const int e2 = e1 + D / 2;
+  const int e1 = h * dh + c * 8;
+  const int e2 = e1 + dh / 2;
 
   const T* in = reinterpret_cast<const T*>(sd.in) + b * sd.in_bs + row0 * sd.in_ls;
   Vec8<T> x1[R], x2[R];
@@ -403,10 +413,9 @@ __device__ __forceinline__ void norm_rope_rows(const NormRopeSide& qs, const Nor
   }
 }
 
-template <typename T, typename TT>
-__global__ void __launch_bounds__(256) qk_norm_rope_kernel(NormRopeSide qs, NormRopeSide ks,
-                                                           int H, int D, int B, int nsides) {
-  norm_rope_rows<T, TT>(qs, ks, H, D, B, nsides, blockIdx.x);
+template <typename T, typename TT, int CPD>
+__global__ void __launch_bounds__(256) qk_norm_rope_kernel(NormRopeSide qs, NormRopeSide ks, int H, int D) {
+  norm_rope_rows<T, TT, CPD>(qs, ks, H, D, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // V [B, L, H, DV] bf16 rows into a key-major bf16 store, 64-token tiles.
@@ -424,13 +433,15 @@ struct VKeyAppend {
 // norm rows drain instead of waiting for a second launch.
 template <typename TT, int DV>
 __global__ void __launch_bounds__(256) qk_norm_rope_v_kernel(NormRopeSide qs, NormRopeSide ks, int H, int D,
-                                                             int B, int nsides, int64_t n_norm, VKeyAppend va) {
+                                                             int nsides, int64_t v_tiles, VKeyAppend va) {
   __shared__ uint16_t tile[transpose_lds_elems<DV>()];
-  if ((int64_t)blockIdx.x < n_norm) {  // uniform across the block
-    norm_rope_rows<uint16_t, TT>(qs, ks, H, D, B, nsides, blockIdx.x);
+  if ((int)blockIdx.z < nsides) {  // uniform across the block
+    norm_rope_rows<uint16_t, TT, DV / 16>(qs, ks, H, D, blockIdx.x, blockIdx.y, blockIdx.z);
     return;
   }
-  const int64_t t = (int64_t)blockIdx.x - n_norm;
+  // the z slices after the norm's: V tiles in linear order
+  const int64_t t = ((int64_t)(blockIdx.z - nsides) * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+  if (t >= v_tiles) return;
   const int64_t ntx = (va.L + kTransposeTokens - 1) / kTransposeTokens;
   const int64_t hb = t / ntx;
   kv_transpose_tile<uint16_t, DV>(va.src, va.s_bs, va.s_ls, va.s_hs, va.dst, va.d_bs, va.d_hs, va.d_ds, va.L,
@@ -498,11 +509,11 @@ extern "C" int ltx_rope_table(void* cos_out, void* sin_out, int out_dtype, const
 namespace {
 
 // Validated launch of the norm rows: the per-side arguments, block size and
-// grid (nblocks = 0: no rows).
+// grid (gx, B, nsides); gx = 0: no rows.
 struct NormLaunch {
   NormRopeSide qs, ks;
   int threads, nsides;
-  int64_t nblocks;
+  int64_t gx;
 };
 
 int norm_setup(int dtype, int64_t B, int64_t H, int64_t D,
@@ -558,20 +569,12 @@ int norm_setup(int dtype, int64_t B, int64_t H, int64_t D,
   NormRopeSide ks{k_in, k_out, gamma_k, k_cos, k_sin, k_in ? k_len : 0, k_in_bs, k_in_ls, k_out_bs,
                   k_out_ls, k_tb, k_th, k_tt, eps_k};
   const int64_t rows = k_in ? (q_len > k_len ? q_len : k_len) : q_len;
-  if (rows == 0) {
-    nl->nblocks = 0;
-    return LTX_OK;
-  }
   LTX_REQUIRE(rows <= 0x7FFFFFFF, "ltx_qk_rmsnorm_rope: too many rows");
-  const int nsides = k_in ? 2 : 1;
-  const int64_t groups = ceil_div(rows, NR_ROWS);
-  const int64_t nblocks = ceil_div(groups, 8) * 8 * B * nsides;
-  LTX_REQUIRE(nblocks <= 0x7FFFFFFF, "ltx_qk_rmsnorm_rope: grid too large");
   nl->qs = qs;
   nl->ks = ks;
   nl->threads = (int)threads;
-  nl->nsides = nsides;
-  nl->nblocks = nblocks;
+  nl->nsides = k_in ? 2 : 1;
+  nl->gx = rows == 0 ? 0 : norm_grid_x(rows);
   return LTX_OK;
 }
 
@@ -594,26 +597,25 @@ extern "C" int ltx_qk_rmsnorm_rope(int dtype, int64_t B, int64_t H, int64_t D,
   const int rc = norm_setup(dtype, B, H, D, q_in, q_len, q_in_bs, q_in_ls, q_out, q_out_bs, q_out_ls, gamma_q, eps_q, q_cos, q_sin,
                        q_tb, q_th, q_tt, k_in, k_len, k_in_bs, k_in_ls, k_out, k_out_bs, k_out_ls, gamma_k, eps_k,
                        k_cos, k_sin, k_tb, k_th, k_tt, tab_dtype, &nl);
-  if (rc != LTX_OK || nl.nblocks == 0) return rc;
+  if (rc != LTX_OK || nl.gx == 0) return rc;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid((unsigned)nl.nblocks), block((unsigned)nl.threads);
+  const dim3 grid((unsigned)nl.gx, (unsigned)B, (unsigned)nl.nsides), block((unsigned)nl.threads);
   const NormRopeSide &qs = nl.qs, &ks = nl.ks;
-  const int nsides = nl.nsides;
+#define LTX_NR(T, TT)                                                                                        \
+  do {                                                                                                       \
+    if (D == 128)                                                                                            \
+      hipLaunchKernelGGL((qk_norm_rope_kernel<T, TT, 8>), grid, block, 0, st, qs, ks, (int)H, (int)D);      \
+    else if (D == 64)                                                                                        \
+      hipLaunchKernelGGL((qk_norm_rope_kernel<T, TT, 4>), grid, block, 0, st, qs, ks, (int)H, (int)D);      \
+    else                                                                                                     \
+      hipLaunchKernelGGL((qk_norm_rope_kernel<T, TT, 0>), grid, block, 0, st, qs, ks, (int)H, (int)D);      \
+  } while (0)
   if (dtype == LTX_BF16) {
-    if (tab_dtype == LTX_BF16)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<uint16_t, uint16_t>), grid, block, 0, st, qs, ks, (int)H, (int)D,
-                         (int)B, nsides);
-    else
-      hipLaunchKernelGGL((qk_norm_rope_kernel<uint16_t, float>), grid, block, 0, st, qs, ks, (int)H, (int)D,
-                         (int)B, nsides);
+    if (tab_dtype == LTX_BF16) LTX_NR(uint16_t, uint16_t); else LTX_NR(uint16_t, float);
   } else {
-    if (tab_dtype == LTX_BF16)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<float, uint16_t>), grid, block, 0, st, qs, ks, (int)H, (int)D,
-                         (int)B, nsides);
-    else
-      hipLaunchKernelGGL((qk_norm_rope_kernel<float, float>), grid, block, 0, st, qs, ks, (int)H, (int)D,
-                         (int)B, nsides);
+    if (tab_dtype == LTX_BF16) LTX_NR(float, uint16_t); else LTX_NR(float, float);
   }
+#undef LTX_NR
   LTX_LAUNCH_CHECK("ltx_qk_rmsnorm_rope");
   return LTX_OK;
 }
@@ -649,18 +651,23 @@ extern "C" int ltx_qk_rmsnorm_rope_v(int dtype, int64_t B, int64_t H, int64_t D,
                        k_cos, k_sin, k_tb, k_th, k_tt, tab_dtype, &nl);
   if (rc != LTX_OK) return rc;
   const int64_t v_tiles = ceil_div(v_len, kTransposeTokens) * H * B;
-  const int64_t nblocks = nl.nblocks + v_tiles;
-  if (nblocks == 0) return LTX_OK;
-  LTX_REQUIRE(nblocks <= 0x7FFFFFFF, "ltx_qk_rmsnorm_rope_v: grid too large");
+  if (nl.gx == 0 && v_tiles == 0) return LTX_OK;
+  // norm slices z < nsides (none without rows), then enough (gx, B) slices
+  // for the V tiles
+  const int64_t gx = nl.gx > 0 ? nl.gx : 8;
+  const int nsides = nl.gx > 0 ? nl.nsides : 0;
+  const int64_t vz = ceil_div(v_tiles, gx * B);
+  LTX_REQUIRE(gx <= 0x7FFFFFFF && nsides + vz <= 65535, "ltx_qk_rmsnorm_rope_v: grid too large");
   const VKeyAppend va{(const uint16_t*)v_src, v_bs, v_ls, v_hs, (uint16_t*)v_dst, vd_bs, vd_hs, vd_ds, v_len,
                       (int)H};
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   // the V tiles run with the norm's block size (a multiple of 64 threads up to
   // 256, or 16 / 32): kv_transpose_tile strides by blockDim
-  const dim3 grid((unsigned)nblocks), block((unsigned)(nl.nblocks > 0 ? nl.threads : 256));
+  const dim3 grid((unsigned)gx, (unsigned)B, (unsigned)(nsides + vz));
+  const dim3 block((unsigned)(nl.gx > 0 ? nl.threads : 256));
 #define LTX_NRV(TT, DV)                                                                                  \
   hipLaunchKernelGGL((qk_norm_rope_v_kernel<TT, DV>), grid, block, 0, st, nl.qs, nl.ks, (int)H, (int)D, \
-                     (int)B, nl.nsides, nl.nblocks, va)
+                     nsides, v_tiles, va)
   if (tab_dtype == LTX_BF16) {
     if (D == 128) LTX_NRV(uint16_t, 128); else LTX_NRV(uint16_t, 64);
   } else {

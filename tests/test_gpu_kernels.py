@@ -219,7 +219,8 @@ def test_kv_append_fp8_bit_exact(dev, shape, frame):
 
 
 @pytest.mark.parametrize("shape,frame", [((2, 1152, 32, 128), 384), ((1, 128, 8, 64), 64),
-                                          ((1, 1024, 4, 128), 512)])
+                                          ((1, 1024, 4, 128), 512), ((2, 150, 32, 64), 25),
+                                          ((1, 96, 3, 128), 96)])
 def test_kv_append_fp8_pair_bit_exact(dev, shape, frame):
     """K and V of a chunk quantised in one launch into arena slot views (offset
     spans of a larger store, V read through a strided projection view): codes

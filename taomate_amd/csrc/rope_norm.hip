@@ -4,6 +4,8 @@
 // it once with 16-byte vector loads, reduces its sum of squares across the
 // workgroup, and writes the normalised, rotated row once.
 
+#include <type_traits>
+
 #include "ltx_common.h"
 #include "kv_transpose.h"
 
@@ -249,8 +251,9 @@ __device__ __forceinline__ float rnd(float v) {
 }
 
 // Rows handled by one workgroup (all loads of its rows are issued before the
-// first reduction).
-constexpr int NR_ROWS = 2;
+// first reduction).  Measured at 1152 rows x 4096, B = 2, with the division-free
+// grid below: 1 row 15.4 us, 2 rows 16.1 us (13.7 / 14.3 with the FAST form).
+constexpr int NR_ROWS = 1;
 
 // Norm grid: blockIdx = (row group, batch, side 0 = q / 1 = k), gridDim.x a
 // multiple of 8.  Workgroups are dispatched round-robin over the 8 XCDs in
@@ -283,15 +286,23 @@ __device__ __forceinline__ NormRopeSide pick_side(const NormRopeSide& q, const N
 
 // The NR_ROWS rows of row group ``rg`` of (batch b, side); every thread of the
 // block calls it (one barrier when normalising).  CPD: D / 16 when known at
-// compile time (8 for D = 128, 4 for D = 64), 0 otherwise.
-template <typename T, typename TT, int CPD>
+// compile time (8 for D = 128, 4 for D = 64), 0 otherwise.  FAST: every side
+// has a norm (eps >= 0), a gamma and RoPE tables, and every element offset
+// of its rows and tables fits in 31 bits (the host checks both), so the
+// loads are issued without flag branches and the addresses are computed in
+// 32-bit arithmetic (measured 16.1 -> 14.3 us at 1152 x 4096, B = 2).
+template <typename T, typename TT, int CPD, bool FAST>
 __device__ __forceinline__ void norm_rope_rows(const NormRopeSide& qs, const NormRopeSide& ks, int H, int D,
                                                int64_t rg, int b, int side) {
   constexpr int R = NR_ROWS;
+  using Off = std::conditional_t<FAST, int32_t, int64_t>;
   const NormRopeSide sd = pick_side(qs, ks, side != 0);
-  const int64_t row0 = rg * R;
-  if (row0 >= sd.len) return;  // uniform across the block
-  const int nr = (int)(sd.len - row0 < R ? sd.len - row0 : R);
+  const int64_t row0l = rg * R;
+  if (row0l >= sd.len) return;  // uniform across the block
+  const int nr = (int)(sd.len - row0l < R ? sd.len - row0l : R);
+  const Off row0 = (Off)row0l;
+  const Off in_bs = (Off)sd.in_bs, in_ls = (Off)sd.in_ls, out_bs = (Off)sd.out_bs, out_ls = (Off)sd.out_ls;
+  const Off tb = (Off)sd.tb, th = (Off)sd.th, tt = (Off)sd.tt;
   const int HD = H * D;
   const int cpd = CPD > 0 ? CPD : D / 16;  // chunks of 8 pairs per head
   const int dh = CPD > 0 ? CPD * 16 : D;
@@ -301,28 +312,29 @@ __device__ __forceinline__ void norm_rope_rows(const NormRopeSide& qs, const Nor
   const int e1 = h * dh + c * 8;
   const int e2 = e1 + dh / 2;
 
-  const T* in = reinterpret_cast<const T*>(sd.in) + b * sd.in_bs + row0 * sd.in_ls;
+  const T* in = reinterpret_cast<const T*>(sd.in) + ((Off)b * in_bs + row0 * in_ls);
   Vec8<T> x1[R], x2[R];
 #pragma unroll
   for (int r = 0; r < R; ++r)
     if (r < nr) {
-      x1[r].load(in + r * sd.in_ls + e1);
-      x2[r].load(in + r * sd.in_ls + e2);
+      x1[r].load(in + ((Off)r * in_ls + e1));
+      x2[r].load(in + ((Off)r * in_ls + e2));
     }
-  const bool rope = sd.cos != nullptr;
+  const bool rope = FAST || sd.cos != nullptr;
   Vec8<TT> cv[R], sv[R];
   if (rope) {
-    const TT* cp = reinterpret_cast<const TT*>(sd.cos) + b * sd.tb + h * sd.th + row0 * sd.tt + c * 8;
-    const TT* sp = reinterpret_cast<const TT*>(sd.sin) + b * sd.tb + h * sd.th + row0 * sd.tt + c * 8;
+    const Off t0 = (Off)b * tb + (Off)h * th + row0 * tt + c * 8;
+    const TT* cp = reinterpret_cast<const TT*>(sd.cos) + t0;
+    const TT* sp = reinterpret_cast<const TT*>(sd.sin) + t0;
 #pragma unroll
     for (int r = 0; r < R; ++r)
       if (r < nr) {
-        cv[r].load(cp + r * sd.tt);
-        sv[r].load(sp + r * sd.tt);
+        cv[r].load(cp + (Off)r * tt);
+        sv[r].load(sp + (Off)r * tt);
       }
   }
-  const bool norm = sd.eps >= 0.0f;
-  const bool has_gamma = norm && sd.gamma != nullptr;
+  const bool norm = FAST || sd.eps >= 0.0f;
+  const bool has_gamma = FAST || (norm && sd.gamma != nullptr);
   Vec8<T> g1, g2;
   if (has_gamma) {
     g1.load(reinterpret_cast<const T*>(sd.gamma) + e1);
@@ -366,7 +378,7 @@ __device__ __forceinline__ void norm_rope_rows(const NormRopeSide& qs, const Nor
     }
   }
 
-  T* out = reinterpret_cast<T*>(sd.out) + b * sd.out_bs + row0 * sd.out_ls;
+  T* out = reinterpret_cast<T*>(sd.out) + ((Off)b * out_bs + row0 * out_ls);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     if (r >= nr) break;
@@ -408,14 +420,14 @@ __device__ __forceinline__ void norm_rope_rows(const NormRopeSide& qs, const Nor
       x1[r].set(i, v1[i]);
       x2[r].set(i, v2[i]);
     }
-    x1[r].store(out + r * sd.out_ls + e1);
-    x2[r].store(out + r * sd.out_ls + e2);
+    x1[r].store(out + ((Off)r * out_ls + e1));
+    x2[r].store(out + ((Off)r * out_ls + e2));
   }
 }
 
-template <typename T, typename TT, int CPD>
+template <typename T, typename TT, int CPD, bool FAST>
 __global__ void __launch_bounds__(256) qk_norm_rope_kernel(NormRopeSide qs, NormRopeSide ks, int H, int D) {
-  norm_rope_rows<T, TT, CPD>(qs, ks, H, D, blockIdx.x, blockIdx.y, blockIdx.z);
+  norm_rope_rows<T, TT, CPD, FAST>(qs, ks, H, D, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // V [B, L, H, DV] bf16 rows into a key-major bf16 store, 64-token tiles.
@@ -431,12 +443,12 @@ struct VKeyAppend {
 // key-major append of the chunk's V (the blocks after, one per (token tile,
 // head, batch)): both stream HBM, and the V tiles fill the CUs while the
 // norm rows drain instead of waiting for a second launch.
-template <typename TT, int DV>
+template <typename TT, int DV, bool FAST>
 __global__ void __launch_bounds__(256) qk_norm_rope_v_kernel(NormRopeSide qs, NormRopeSide ks, int H, int D,
                                                              int nsides, int64_t v_tiles, VKeyAppend va) {
   __shared__ uint16_t tile[transpose_lds_elems<DV>()];
   if ((int)blockIdx.z < nsides) {  // uniform across the block
-    norm_rope_rows<uint16_t, TT, DV / 16>(qs, ks, H, D, blockIdx.x, blockIdx.y, blockIdx.z);
+    norm_rope_rows<uint16_t, TT, DV / 16, FAST>(qs, ks, H, D, blockIdx.x, blockIdx.y, blockIdx.z);
     return;
   }
   // the z slices after the norm's: V tiles in linear order
@@ -514,7 +526,24 @@ struct NormLaunch {
   NormRopeSide qs, ks;
   int threads, nsides;
   int64_t gx;
+  bool fast;  // bf16 rows, every side normalised with gamma and rotated, 31-bit offsets
 };
+
+// Whether one side qualifies for the FAST kernel form (see norm_rope_rows).
+bool side_is_fast(const NormRopeSide& s, int64_t B, int64_t H, int64_t D) {
+  if (s.len == 0) return true;
+  if (!s.cos || !s.gamma || !(s.eps >= 0.0f)) return false;
+  if (s.in_bs < 0 || s.in_ls < 0 || s.out_bs < 0 || s.out_ls < 0 || s.tb < 0 || s.th < 0 || s.tt < 0)
+    return false;
+  const int64_t lim = 0x7FFFFFFF;
+  auto fits = [&](int64_t v) { return v >= 0 && v <= lim; };
+  // strides below 2^31 keep every product below 2^62 (no int64 overflow)
+  for (int64_t st : {s.in_bs, s.in_ls, s.out_bs, s.out_ls, s.tb, s.th, s.tt})
+    if (!fits(st)) return false;
+  return fits((B - 1) * s.in_bs + (s.len - 1) * s.in_ls + H * D) &&
+         fits((B - 1) * s.out_bs + (s.len - 1) * s.out_ls + H * D) &&
+         fits((B - 1) * s.tb + (H - 1) * s.th + (s.len - 1) * s.tt + D / 2);
+}
 
 int norm_setup(int dtype, int64_t B, int64_t H, int64_t D,
                       const void* q_in, int64_t q_len, int64_t q_in_bs, int64_t q_in_ls,
@@ -575,6 +604,7 @@ int norm_setup(int dtype, int64_t B, int64_t H, int64_t D,
   nl->threads = (int)threads;
   nl->nsides = k_in ? 2 : 1;
   nl->gx = rows == 0 ? 0 : norm_grid_x(rows);
+  nl->fast = dtype == LTX_BF16 && side_is_fast(qs, B, H, D) && side_is_fast(ks, B, H, D);
   return LTX_OK;
 }
 
@@ -601,19 +631,23 @@ extern "C" int ltx_qk_rmsnorm_rope(int dtype, int64_t B, int64_t H, int64_t D,
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)nl.gx, (unsigned)B, (unsigned)nl.nsides), block((unsigned)nl.threads);
   const NormRopeSide &qs = nl.qs, &ks = nl.ks;
-#define LTX_NR(T, TT)                                                                                        \
+#define LTX_NR(T, TT, F)                                                                                     \
   do {                                                                                                       \
     if (D == 128)                                                                                            \
-      hipLaunchKernelGGL((qk_norm_rope_kernel<T, TT, 8>), grid, block, 0, st, qs, ks, (int)H, (int)D);      \
+      hipLaunchKernelGGL((qk_norm_rope_kernel<T, TT, 8, F>), grid, block, 0, st, qs, ks, (int)H, (int)D);   \
     else if (D == 64)                                                                                        \
-      hipLaunchKernelGGL((qk_norm_rope_kernel<T, TT, 4>), grid, block, 0, st, qs, ks, (int)H, (int)D);      \
+      hipLaunchKernelGGL((qk_norm_rope_kernel<T, TT, 4, F>), grid, block, 0, st, qs, ks, (int)H, (int)D);   \
     else                                                                                                     \
-      hipLaunchKernelGGL((qk_norm_rope_kernel<T, TT, 0>), grid, block, 0, st, qs, ks, (int)H, (int)D);      \
+      hipLaunchKernelGGL((qk_norm_rope_kernel<T, TT, 0, F>), grid, block, 0, st, qs, ks, (int)H, (int)D);   \
   } while (0)
   if (dtype == LTX_BF16) {
-    if (tab_dtype == LTX_BF16) LTX_NR(uint16_t, uint16_t); else LTX_NR(uint16_t, float);
+    if (tab_dtype == LTX_BF16) {
+      if (nl.fast) LTX_NR(uint16_t, uint16_t, true); else LTX_NR(uint16_t, uint16_t, false);
+    } else {
+      if (nl.fast) LTX_NR(uint16_t, float, true); else LTX_NR(uint16_t, float, false);
+    }
   } else {
-    if (tab_dtype == LTX_BF16) LTX_NR(float, uint16_t); else LTX_NR(float, float);
+    if (tab_dtype == LTX_BF16) LTX_NR(float, uint16_t, false); else LTX_NR(float, float, false);
   }
 #undef LTX_NR
   LTX_LAUNCH_CHECK("ltx_qk_rmsnorm_rope");
@@ -665,9 +699,15 @@ extern "C" int ltx_qk_rmsnorm_rope_v(int dtype, int64_t B, int64_t H, int64_t D,
   // 256, or 16 / 32): kv_transpose_tile strides by blockDim
   const dim3 grid((unsigned)gx, (unsigned)B, (unsigned)(nsides + vz));
   const dim3 block((unsigned)(nl.gx > 0 ? nl.threads : 256));
-#define LTX_NRV(TT, DV)                                                                                  \
-  hipLaunchKernelGGL((qk_norm_rope_v_kernel<TT, DV>), grid, block, 0, st, nl.qs, nl.ks, (int)H, (int)D, \
-                     nsides, v_tiles, va)
+#define LTX_NRV(TT, DV)                                                                                           \
+  do {                                                                                                            \
+    if (nl.fast)                                                                                                  \
+      hipLaunchKernelGGL((qk_norm_rope_v_kernel<TT, DV, true>), grid, block, 0, st, nl.qs, nl.ks, (int)H, (int)D, \
+                         nsides, v_tiles, va);                                                                    \
+    else                                                                                                          \
+      hipLaunchKernelGGL((qk_norm_rope_v_kernel<TT, DV, false>), grid, block, 0, st, nl.qs, nl.ks, (int)H,       \
+                         (int)D, nsides, v_tiles, va);                                                            \
+  } while (0)
   if (tab_dtype == LTX_BF16) {
     if (D == 128) LTX_NRV(uint16_t, 128); else LTX_NRV(uint16_t, 64);
   } else {

@@ -121,6 +121,35 @@ def test_attention_with_cache_layer(dev, case, packed):
     assert c >= (0.999 if kvd == "fp8" else 0.9999), c
 
 
+@pytest.mark.parametrize("case", LAYERS[:2], ids=[c[0] for c in LAYERS[:2]])
+def test_dense_cache_layer(dev, case):
+    """Plain-tensor caches (no arena plan: the reference's torch.cat caches,
+    kv_cache.py:394-398).  At the 16x24 chunk shape the cached and new V go
+    into one key-major store for the pipelined kernel (1152 queries over
+    3456 + 1152 keys); the 8x12 case (192 queries) concatenates as the
+    reference does.  Both match the fp32 oracle."""
+    name, B, gh, gw, H, Dh, seed, kvd = case
+    d = H * Dh
+    segs = SEGS_SMALL if H == 8 else SEGS_FULL
+    cur_f0, cur_nf = (10, 2) if H == 8 else (12, 3)
+    attn, w = make_layer(dev, d, H, Dh, seed)
+    xs, xc, ref, ref_k = _layer_reference(B, gh, gw, H, Dh, seed, w)
+    kc = vc = None
+    with torch.no_grad():
+        for (nm, f0, nf), x in zip(segs, xs):
+            _, nk, nv = T.attention_with_cache(attn, x.to(dev, torch.bfloat16), None,
+                                               gpu_pe(dev, (nf, gh, gw), d, H, f0, B), None, kc, vc)
+            kc, vc = T._cat_cache(kc, nk), T._cat_cache(vc, nv)
+        out, nk, nv = T.attention_with_cache(attn, xc.to(dev, torch.bfloat16), None,
+                                             gpu_pe(dev, (cur_nf, gh, gw), d, H, cur_f0, B), None, kc, vc)
+    torch.cuda.synchronize()
+    assert not isinstance(kc, T.KVSpanView) and kc.is_contiguous() and vc.is_contiguous()
+    assert nk.shape == (B, cur_nf * gh * gw, H, Dh) and nv.stride(3) == 1
+    assert_bf16_close(out, ref, name + " dense")
+    assert cosine(out, ref) >= 0.9999
+    assert cosine(nk, ref_k) >= 0.9999
+
+
 def test_audio_and_cross_modal_attention(dev):
     """Audio self-attention (75 queries over 600 cached + 75 new audio keys, 32 x 64,
     1-D audio RoPE) and the A2V / V2A cross-modal attentions (1152 video tokens
@@ -184,6 +213,36 @@ def test_text_cross_attention_with_padding_mask(dev):
         out = attn(x.to(dev, torch.bfloat16), context=ctx.to(dev, torch.bfloat16), mask=m.to(dev))
     assert_bf16_close(out, ref, "text cross")
     assert cosine(out, ref) >= 0.9999
+
+
+def test_text_kv_cache_keeps_key_major_v(dev, monkeypatch):
+    """A cache hit of the text K/V attends the cached key-major V as it is: no
+    V transposition runs on the hit (the pipelined kernel's path: >= 256
+    queries, a key-padding mask that keeps the same prefix in every row), and
+    the output equals the uncached one bit for bit."""
+    from taomate_amd import kernels as K
+    B, H, Dh, d = 2, 8, 128, 1024
+    attn, w = make_layer(dev, d, H, Dh, 37, context_dim=d, gate=True)
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(B, 384, d, generator=g).to(dev, torch.bfloat16)
+    ctx = torch.randn(B, 200, d, generator=g).to(dev, torch.bfloat16)
+    keep = torch.ones(B, 200, dtype=torch.int64)
+    keep[:, 160:] = 0
+    m = OA.prepare_attention_mask(keep, torch.bfloat16).to(dev)
+    calls = []
+    real = K.kv_append
+    monkeypatch.setattr(K, "kv_append", lambda *a, **k: (calls.append(1), real(*a, **k))[1])
+    with torch.no_grad():
+        plain = attn(x, context=ctx, mask=m)
+        assert len(calls) == 1                      # the uncached call transposes V once
+        attn.cache_text_kv_()
+        first = attn(x, context=ctx, mask=m)        # fills the entry (one transposition)
+        n_fill = len(calls)
+        again = attn(x, context=ctx, mask=m)        # hit: nothing transposed
+        assert len(calls) == n_fill == 2
+        attn.cache_text_kv_(False)
+    torch.cuda.synchronize()
+    assert torch.equal(first, plain) and torch.equal(again, plain)
 
 
 def test_text_kv_cache_is_exact(dev):

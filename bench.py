@@ -540,6 +540,10 @@ def main():
         append()
     ms_norm = time_region(norm, 50)
     ms_app = time_region(append, 50)
+    # the step's first part on its own: as launched in the step, and as the
+    # two separate launches (norm, then append) it replaces
+    ms_prep_alone = time_region(prep, 50)
+    ms_prep_two = time_region(lambda: (norm(), append()), 50)
     kvb = 1 if args.kv == "fp8" else 2
     fl = attn_flops()
     ach = fl / (ms_attn * 1e-3) / 1e12
@@ -578,6 +582,7 @@ def main():
                       else "K and V quantised to e4m3 into the arena (one launch)"},
         "step_prep": {"ms": ms_prep,
                       "GB/s": (norm_rope_bytes() + append_bytes(args.kv)) / (ms_prep * 1e-3) / 1e9,
+                      "alone_ms": ms_prep_alone, "two_launches_ms": ms_prep_two,
                       "what": "fused q/k norm + RoPE + V append (one launch)" if args.kv == "bf16"
                       else "q/k norm + RoPE, then the fp8 pair append"},
         "per_step_ms": {"step": dist(step_ms), "attention": dist(attn_ms), "prep": dist(prep_ms)},

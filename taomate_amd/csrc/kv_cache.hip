@@ -152,7 +152,7 @@ __global__ void __launch_bounds__(kQuantThreads) kv_quant_kernel(
 // eighth register pair of an earlier version cost the second workgroup).  The
 // quotients are the corrected ones of quotients_e4m3_bf16, the same as
 // kv_quant_kernel's for bf16 sources, so codes and scales are bit-identical
-// to it.
+// to it for finite inputs.
 constexpr int kPairThreads = 1024;
 constexpr int kPairRegs = 6;
 
@@ -168,26 +168,38 @@ struct QuantPair {
   int B, frame_tokens, D;
 };
 
-template <int CPR>
+// OFF32: every element offset of the sources and destinations fits in 31 bits
+// (checked on the host), so addresses are computed in 32-bit arithmetic.
+template <int CPR, bool OFF32>
 __global__ void __launch_bounds__(kPairThreads) kv_quant_pair_kernel(const QuantPair a) {
+  using Off = std::conditional_t<OFF32, int32_t, int64_t>;
   const int f = blockIdx.x, h = blockIdx.y;
-  const int which = blockIdx.z >= (unsigned)a.B ? 1 : 0;
-  const int b = blockIdx.z - which * a.B;
-  const QuantTensor& T = a.t[which];
+  const bool second = blockIdx.z >= (unsigned)a.B;
+  const int b = blockIdx.z - (second ? a.B : 0);
+  // per-tensor fields by scalar selects (no indexing of the kernel-argument array)
+  const uint16_t* src = second ? a.t[1].src : a.t[0].src;
+  uint8_t* dst = second ? a.t[1].dst : a.t[0].dst;
+  float* scales = second ? a.t[1].scales : a.t[0].scales;
+  const Off s_ls = (Off)(second ? a.t[1].s_ls : a.t[0].s_ls);
+  const Off s_off = (Off)b * (Off)(second ? a.t[1].s_bs : a.t[0].s_bs) + (Off)h * (Off)(second ? a.t[1].s_hs : a.t[0].s_hs);
+  const Off d_ls = (Off)a.d_ls;
   const int cpr = CPR > 0 ? CPR : a.D / 8;
   const int n = a.frame_tokens * cpr;
-  const int64_t l0 = (int64_t)f * a.frame_tokens;
-  const uint16_t* sbase = T.src + b * T.s_bs + l0 * T.s_ls + h * T.s_hs;
-  uint8_t* dbase = T.dst + b * a.d_bs + l0 * a.d_ls + h * a.d_hs;
+  const Off l0 = (Off)f * a.frame_tokens;
+  const uint16_t* sbase = src + (s_off + l0 * s_ls);
+  uint8_t* dbase = dst + ((Off)b * (Off)a.d_bs + l0 * d_ls + (Off)h * (Off)a.d_hs);
   auto load = [&](int idx) {
     const int t = idx / cpr, c = idx % cpr;
-    return *reinterpret_cast<const uint4*>(sbase + (int64_t)t * T.s_ls + c * 8);
+    return *reinterpret_cast<const uint4*>(sbase + ((Off)t * s_ls + c * 8));
   };
-  auto amax8 = [&](uint4 r, float m) {
+  // absmax as the largest bf16 magnitude, two values per packed 16-bit max
+  // (magnitude bits order as the values; a NaN in the frame gives a NaN
+  // scale, as a float amax would)
+  typedef unsigned short ushort2_t __attribute__((ext_vector_type(2)));
+  auto amax8 = [&](uint4 r, ushort2_t m) {
     const uint32_t w[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      m = fmaxf(m, fmaxf(fabsf(bf16_bits_to_f32(w[i] & 0xFFFFu)), fabsf(bf16_bits_to_f32(w[i] >> 16))));
+    for (int i = 0; i < 4; ++i) m = __builtin_elementwise_max(m, __builtin_bit_cast(ushort2_t, w[i] & 0x7FFF7FFFu));
     return m;
   };
   auto store = [&](int idx, uint4 r, float sc, float rc, bool corrected) {
@@ -200,7 +212,7 @@ __global__ void __launch_bounds__(kPairThreads) kv_quant_pair_kernel(const Quant
     }
     quotients_e4m3_bf16(x, sc, rc, corrected, q);
     const int t = idx / cpr, c = idx % cpr;
-    *reinterpret_cast<uint2*>(dbase + (int64_t)t * a.d_ls + c * 8) =
+    *reinterpret_cast<uint2*>(dbase + ((Off)t * d_ls + c * 8)) =
         make_uint2(pack4_e4m3(q[0], q[1], q[2], q[3]), pack4_e4m3(q[4], q[5], q[6], q[7]));
   };
 
@@ -210,26 +222,31 @@ __global__ void __launch_bounds__(kPairThreads) kv_quant_pair_kernel(const Quant
     const int idx = threadIdx.x + i * kPairThreads;
     raw[i] = idx < n ? load(idx) : make_uint4(0, 0, 0, 0);
   }
-  float amax = 0.0f;
+  ushort2_t am = {0, 0};
 #pragma unroll
-  for (int i = 0; i < kPairRegs; ++i) amax = amax8(raw[i], amax);
+  for (int i = 0; i < kPairRegs; ++i) am = amax8(raw[i], am);
   // keep only the raw chunks live across the reduction (the quantise pass
   // converts them again instead of holding 8 floats per chunk)
 #pragma unroll
   for (int i = 0; i < kPairRegs; ++i)
     asm volatile("" : "+v"(raw[i].x), "+v"(raw[i].y), "+v"(raw[i].z), "+v"(raw[i].w));
-  for (int idx = threadIdx.x + kPairRegs * kPairThreads; idx < n; idx += kPairThreads) amax = amax8(load(idx), amax);
+  for (int idx = threadIdx.x + kPairRegs * kPairThreads; idx < n; idx += kPairThreads) am = amax8(load(idx), am);
+  uint32_t mbits = am.x > am.y ? am.x : am.y;
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint32_t o = (uint32_t)__shfl_xor((int)mbits, off, 64);
+    mbits = o > mbits ? o : mbits;
+  }
   constexpr int kWaves = kPairThreads / 64;
-  __shared__ float red[kWaves];
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __shared__ uint32_t red[kWaves];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mbits;
   __syncthreads();
-  float m = red[0];
+  uint32_t mb = red[0];
 #pragma unroll
-  for (int w = 1; w < kWaves; ++w) m = fmaxf(m, red[w]);
-  const float sc = m > 0.0f ? __fdiv_rn(m, 448.0f) : 1.0f;
-  if (threadIdx.x == 0) T.scales[b * a.sc_bs + h * a.sc_hs + f] = sc;
+  for (int w = 1; w < kWaves; ++w) mb = red[w] > mb ? red[w] : mb;
+  const float m = bf16_bits_to_f32(mb);
+  const float sc = m == 0.0f ? 1.0f : __fdiv_rn(m, 448.0f);
+  if (threadIdx.x == 0) scales[b * a.sc_bs + h * a.sc_hs + f] = sc;
   const float rc = __fdiv_rn(1.0f, sc);
   const bool corrected = m >= kCorrectedMinMax;
 #pragma unroll
@@ -241,14 +258,35 @@ __global__ void __launch_bounds__(kPairThreads) kv_quant_pair_kernel(const Quant
     store(idx, load(idx), sc, rc, corrected);
 }
 
+// Whether every element offset the pair kernel forms fits in 31 bits.
+inline bool pair_offsets_fit(const QuantPair& a, int ntensors, int64_t L, int64_t H) {
+  const int64_t lim = 0x7FFFFFFF;
+  auto ok = [&](int64_t bs, int64_t ls, int64_t hs) {
+    if (bs < 0 || ls < 0 || hs < 0 || bs > lim || ls > lim || hs > lim) return false;
+    return (a.B - 1) * bs + (L - 1) * ls + (H - 1) * hs + a.D <= lim;
+  };
+  for (int t = 0; t < ntensors; ++t)
+    if (!ok(a.t[t].s_bs, a.t[t].s_ls, a.t[t].s_hs)) return false;
+  return ok(a.d_bs, a.d_ls, a.d_hs);
+}
+
 inline int launch_quant_pair(const QuantPair& a, int ntensors, int64_t L, int64_t H, hipStream_t st) {
   const dim3 grid((unsigned)(L / a.frame_tokens), (unsigned)H, (unsigned)(a.B * ntensors));
+  const bool off32 = pair_offsets_fit(a, ntensors, L, H);
+#define LTX_QP(CPR)                                                                        \
+  do {                                                                                     \
+    if (off32)                                                                             \
+      hipLaunchKernelGGL((kv_quant_pair_kernel<CPR, true>), grid, dim3(kPairThreads), 0, st, a);  \
+    else                                                                                   \
+      hipLaunchKernelGGL((kv_quant_pair_kernel<CPR, false>), grid, dim3(kPairThreads), 0, st, a); \
+  } while (0)
   if (a.D == 128)
-    hipLaunchKernelGGL(kv_quant_pair_kernel<16>, grid, dim3(kPairThreads), 0, st, a);
+    LTX_QP(16);
   else if (a.D == 64)
-    hipLaunchKernelGGL(kv_quant_pair_kernel<8>, grid, dim3(kPairThreads), 0, st, a);
+    LTX_QP(8);
   else
-    hipLaunchKernelGGL(kv_quant_pair_kernel<0>, grid, dim3(kPairThreads), 0, st, a);
+    LTX_QP(0);
+#undef LTX_QP
   return LTX_OK;
 }
 

@@ -96,14 +96,17 @@ __device__ __forceinline__ void quotients_for_e4m3(const float (&x)[N], float sc
 constexpr float kCorrectedMinMax = 0x1p-96f;
 
 // fl(x / sc) up to last bits that cannot change an e4m3 code (see
-// kCorrectedMinMax): q = fl(x * r) for r = fl(1 / sc), the residual x - q * sc
-// in one fused multiply-add, then one correction q + residual * r (Markstein's
-// correction step); the sign is taken from x so that -0 stays -0.  Straight
-// line, one multiply and two FMAs per value.
+// kCorrectedMinMax): q = fl(x * r) for r = fl(1 / sc), the negated residual
+// q * sc - x in one fused multiply-add (round to nearest even is symmetric, so
+// it is exactly minus the residual x - q * sc), then one correction
+// q - negated_residual * r (Markstein's correction step).  Written this way a
+// zero x keeps its sign (x = -0: q = -0, the negated residual +0, and
+// -0 + -0 = -0) without a separate copysign.  Straight line: one multiply
+// and two FMAs per value.
 __device__ __forceinline__ float quotient_e4m3_corrected(float x, float sc, float r) {
   const float q = __fmul_rn(x, r);
-  const float e = __fmaf_rn(-q, sc, x);
-  return copysignf(__fmaf_rn(e, r, q), x);
+  const float ne = __fmaf_rn(q, sc, -x);
+  return __fmaf_rn(-ne, r, q);
 }
 
 // Quotients of a chunk of bf16-sourced values for e4m3 rounding: the corrected

@@ -3,8 +3,8 @@
  * For every positive finite bf16 frame maximum m >= 2^-96 and every bf16 value
  * x with |x| <= m, with sc = fl(m / 448) and r = fl(1 / sc):
  *   q  = fl(x * r)
- *   e  = fma(-q, sc, x)
- *   q1 = copysign(fma(e, r, q), x)
+ *   ne = fma(q, sc, -x)          (minus the residual x - q * sc)
+ *   q1 = fma(-ne, r, q)
  * must give the same OCP e4m3fn code (after clamping to +-448, round to
  * nearest even) as the IEEE quotient fl(x / sc).  Build with
  * -ffp-contract=off so that the compiler adds no contractions.
@@ -64,8 +64,8 @@ int main(int argc, char** argv) {
       const float x = from_bf16((i >> 1) | ((i & 1u) << 15));
       const float exact = x / sc;
       const float q = x * r;
-      const float e = fmaf(-q, sc, x);
-      const float q1 = copysignf(fmaf(e, r, q), x);
+      const float ne = fmaf(q, sc, -x);
+      const float q1 = fmaf(-ne, r, q);
       lp++;
       if (bits_of(q1) != bits_of(exact)) {
         lb++;

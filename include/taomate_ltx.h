@@ -198,7 +198,10 @@ int ltx_kv_gather(int64_t elem_bytes, int64_t B, int64_t H, int64_t D, const voi
  *   get weight 0).  The KV arena guarantees both.
  *   kv_dtype LTX_BF16, or LTX_F8E4M3 (token-major) with per-(b, h, frame)
  *   float32 scales: k_scales[i], v_scales[i] for segment i, index b*sc_bs +
- *   h*sc_hs + (t/frame) where t counts tokens from the segment start.
+ *   h*sc_hs + (t/frame) where t counts tokens from the segment start (a
+ *   segment starts on a frame boundary; any frame_tokens >= 1, a frame that
+ *   is not a multiple of 64 tokens being cut into 64-key tiles at its
+ *   boundaries).
  *   key_mask: NULL or float32 additive mask [B, Lk_total] with batch stride
  *   mask_bs (the reference's `(m - 1) * finfo.max` padding mask,
  *   ltx_causal/transformer/causal_model.py:551-562); token-major V only.

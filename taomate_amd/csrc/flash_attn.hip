@@ -608,12 +608,13 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 //   barrier per tile frees the buffers read in the previous iteration.
 //
 // fp8 K/V (token-major e4m3 codes with per-(batch, head, frame) scales) use
-// the same slot program.  Their tiles are staged through registers instead:
+// the same slot program (tiles cut at frame boundaries, see KeyStreamT).
+// Their tiles are staged through registers instead:
 // each thread loads 8-byte chunks of the next tiles from HBM one iteration
 // ahead, and after the barrier decodes them (exactly) to bf16 into the free
 // LDS buffers, K rows in the swapped order and V transposed with v_perm, so
 // every code is decoded once per workgroup.  A tile never crosses a frame
-// (frames are whole tiles), so its scales are two scalars: the K scale joins
+// (KeyStreamT<true>), so its scales are two scalars: the K scale joins
 // the logit scale, c_j = c * sk_j, and the V scale joins the exponent,
 // P' = 2^(S c_j - m + log2 sv_j) = sv_j P, so the PV MFMAs read plain codes;
 // the row sum and the overflow check use sum(P') / sv_j.
@@ -624,13 +625,21 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // tile on, and the byte address of the current tile's first key (segment base
 // + the (b, h) offset + the rows already passed).  Total keys < 2^31 (checked
 // on the host).
-struct KeyStream {
-  int s, rem;
+//
+// FRAMED (fp8 K/V, one scale per frame): tiles never cross a frame.  A frame
+// of F tokens is cut into ceil(F / 64) tiles, the last one partial when F is
+// not a multiple of 64, and a segment's last frame may itself be partial; a
+// segment starts on a frame boundary (frame-aligned arena spans).  frem holds
+// the keys of the current frame from the current tile on.
+template <bool FRAMED>
+struct KeyStreamT {
+  int s, rem, frem;
   const char* ptr;
   __device__ __forceinline__ void enter(const void* const* base, int64_t head, const FlashParams& p, int seg) {
     s = seg;
     rem = (int)(p.seg_start[seg + 1] - p.seg_start[seg]);
     ptr = reinterpret_cast<const char*>(base[seg]) + head;
+    if constexpr (FRAMED) frem = p.frame;
   }
   __device__ __forceinline__ void seek(const void* const* base, int64_t head, int64_t tile_bytes,
                                        const FlashParams& p, int j) {
@@ -638,24 +647,52 @@ struct KeyStream {
     for (int i = 1; i < p.n_seg; ++i) seg = (j >= p.tile_start[i]) ? i : seg;
     enter(base, head, p, seg);
     const int t = j - p.tile_start[seg];
-    rem -= t * kBN;
-    ptr += t * tile_bytes;
+    if constexpr (FRAMED) {
+      const int tpf = (p.frame + kBN - 1) / kBN;  // tiles per frame
+      const int fr = t / tpf, k = t - fr * tpf;
+      const int pos = fr * p.frame + k * kBN;
+      frem = p.frame - k * kBN;
+      rem -= pos;
+      ptr += (int64_t)pos * (tile_bytes / kBN);
+    } else {
+      rem -= t * kBN;
+      ptr += t * tile_bytes;
+    }
   }
   __device__ __forceinline__ void next(const void* const* base, int64_t head, int64_t tile_bytes,
                                        const FlashParams& p) {
-    rem -= kBN;
-    ptr += tile_bytes;
+    if constexpr (FRAMED) {
+      const int len = nvalid();
+      rem -= len;
+      ptr += (int64_t)len * (tile_bytes / kBN);
+      frem -= len;
+      if (frem == 0) frem = p.frame;
+    } else {
+      rem -= kBN;
+      ptr += tile_bytes;
+    }
     if (rem <= 0 && s + 1 < p.n_seg) enter(base, head, p, s + 1);
   }
-  __device__ __forceinline__ int nvalid() const { return rem < kBN ? rem : kBN; }
+  __device__ __forceinline__ int nvalid() const {
+    const int n = rem < kBN ? rem : kBN;
+    if constexpr (FRAMED) return frem < n ? frem : n;
+    return n;
+  }
   // first key of the current tile, counted from its segment's start
   __device__ __forceinline__ int row0(const FlashParams& p) const {
     return (int)(p.seg_start[s + 1] - p.seg_start[s]) - rem;
   }
 };
 
-template <int D, bool FP8>
-__global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParams p) {
+// The pipelined kernels' body.  FRAMED (fp8 only): frames that are not a
+// whole number of 64-key tiles, cut at frame boundaries (KeyStreamT<true>,
+// its own kernel); frames of 64k tokens take the plain tiling, which never
+// crosses a frame either and keeps the hot kernel's scalar state and
+// registers as they were (the framed state costs the D = 128 instance
+// register spills).
+template <int D, bool FP8, bool FRAMED>
+__device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
+  static_assert(FP8 || !FRAMED, "frame tiling is an fp8 feature");
   constexpr int BM = kBM, BN = kBN;
   constexpr int NKC = D / 8;
   constexpr int KS = D + 8;
@@ -718,7 +755,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
   const int64_t v_head = FP8 ? k_head : (b * p.v_bs + h * p.v_hs) * 2;
   const int64_t k_tile = (int64_t)BN * row_bytes;
   const int64_t v_tile = FP8 ? k_tile : BN * 2;
-  KeyStream kit, vit;
+  KeyStreamT<FRAMED> kit, vit;
   kit.seek(p.k_ptr, k_head, k_tile, p, wi.j0);
   vit.seek(p.v_ptr, v_head, v_tile, p, wi.j0);
   // LDS address of this wave's first load slot in a buffer; the empty asm
@@ -838,7 +875,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
     }
   };
   // the tile the softmax works on: its valid keys and (fp8) its scales
-  KeyStream cit;
+  KeyStreamT<FRAMED> cit;
   if constexpr (FP8) cit.seek(p.k_ptr, 0, 0, p, wi.j0);
   struct TileScale { float c, off, inv; };  // logit scale, exponent offset log2 sv, 1 / sv
   auto tile_scale = [&]() -> TileScale {
@@ -1105,6 +1142,17 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
                  pair_sum(l_run));
 }
 
+template <int D, bool FP8>
+__global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParams p) {
+  flash_pipe_body<D, FP8, false>(p);
+}
+
+// fp8 frames that are not a whole number of 64-key tiles
+template <int D>
+__global__ void __launch_bounds__(256, 2) flash_fwd_pipe_framed_kernel(const FlashParams p) {
+  flash_pipe_body<D, true, true>(p);
+}
+
 template <int D>
 int launch_combine(const FlashParams& p, hipStream_t st) {
   if (p.split <= 1) return LTX_OK;
@@ -1121,11 +1169,15 @@ inline int64_t grid_blocks(const FlashParams& p) {
   return p.n_full + (nq - p.n_full) * p.split;
 }
 
-template <int D, bool FP8>
+template <int D, bool FP8, bool FRAMED = false>
 int launch_flash_pipe(const FlashParams& p, hipStream_t st) {
+  static_assert(FP8 || !FRAMED, "frame tiling is an fp8 feature");
   const int64_t nblocks = grid_blocks(p);
   LTX_REQUIRE(nblocks <= 0x7FFFFFFF, "ltx_flash_attn_fwd: grid too large");
-  hipLaunchKernelGGL((flash_fwd_pipe_kernel<D, FP8>), dim3((unsigned)nblocks), dim3(256), 0, st, p);
+  if constexpr (FRAMED)
+    hipLaunchKernelGGL((flash_fwd_pipe_framed_kernel<D>), dim3((unsigned)nblocks), dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((flash_fwd_pipe_kernel<D, FP8>), dim3((unsigned)nblocks), dim3(256), 0, st, p);
   LTX_LAUNCH_CHECK("ltx_flash_attn_fwd");
   return launch_combine<D>(p, st);
 }
@@ -1296,16 +1348,21 @@ static int flash_attn_fwd_impl(const void* q, int64_t B, int64_t Lq, int64_t H, 
     if (fp8) {
       LTX_REQUIRE(k_scales && v_scales && k_scales[i] && v_scales[i],
                   "ltx_flash_attn_fwd: fp8 segment %lld needs k/v scales", (long long)i);
-      LTX_REQUIRE(frame_tokens > 0 && frame_tokens % kBN == 0,
-                  "ltx_flash_attn_fwd: fp8 needs frame_tokens to be a multiple of %d (got %lld)", kBN,
-                  (long long)frame_tokens);
+      LTX_REQUIRE(frame_tokens > 0 && frame_tokens <= 0x7FFFFFFF,
+                  "ltx_flash_attn_fwd: fp8 needs frame_tokens > 0 (got %lld)", (long long)frame_tokens);
       p.k_sc[n] = k_scales[i];
       p.v_sc[n] = v_scales[i];
     }
     p.k_ptr[n] = k_ptrs[i];
     p.v_ptr[n] = v_ptrs[i];
     p.seg_start[n + 1] = p.seg_start[n] + seg_lens[i];
-    const int64_t tiles = p.tile_start[n] + (seg_lens[i] + kBN - 1) / kBN;
+    // fp8: tiles never cross a frame (ceil(F / 64) per frame, the segment's
+    // last frame possibly partial); bf16: ceil(len / 64)
+    const int64_t seg_tiles =
+        fp8 ? (seg_lens[i] / frame_tokens) * ((frame_tokens + kBN - 1) / kBN) +
+                  (seg_lens[i] % frame_tokens + kBN - 1) / kBN
+            : (seg_lens[i] + kBN - 1) / kBN;
+    const int64_t tiles = p.tile_start[n] + seg_tiles;
     LTX_REQUIRE(tiles <= 0x7FFFFFFF, "ltx_flash_attn_fwd: too many keys");
     p.tile_start[n + 1] = (int)tiles;
     ++n;
@@ -1351,6 +1408,12 @@ static int flash_attn_fwd_impl(const void* q, int64_t B, int64_t Lq, int64_t H, 
     return launch_flash_pipe<64, false>(p, st);
   }
   if (fp8) {
+    // the framed instances share the plain ones' occupancy (same registers
+    // and LDS), so the split plan above holds for them too
+    if (frame_tokens % kBN != 0) {
+      if (D == 128) return launch_flash_pipe<128, true, true>(p, st);
+      return launch_flash_pipe<64, true, true>(p, st);
+    }
     if (D == 128) return launch_flash_pipe<128, true>(p, st);
     return launch_flash_pipe<64, true>(p, st);
   }

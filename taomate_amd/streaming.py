@@ -89,9 +89,6 @@ class ChunkStream:
                  theta: float = 10000.0, memory_beta: float = 0.15, memory_tether: float = 0.20):
         if window_frames % chunk_frames:
             raise ValueError("window_frames must be a whole number of chunks")
-        if kv_dtype == "fp8" and (int(video_hw[0]) * int(video_hw[1])) % 64:
-            raise ValueError("fp8 K/V keeps one scale per frame and per 64-key tile: a latent frame must "
-                             f"hold a multiple of 64 tokens (got {video_hw[0]}x{video_hw[1]})")
         self.attn = attn
         self.hw = int(video_hw[0]) * int(video_hw[1])
         self.grid = (int(video_hw[0]), int(video_hw[1]))

@@ -463,9 +463,16 @@ def test_flash_attn_key_mask(dev):
 
 
 @pytest.mark.parametrize("case", [(2, 1152, 32, 128, 384, [384, 768, 2304, 1152]),
-                                  (1, 192, 8, 64, 64, [128, 64, 384, 192])],
-                         ids=["16x24grid", "8x12grid"])
+                                  (1, 192, 8, 64, 64, [128, 64, 384, 192]),
+                                  (1, 192, 8, 64, 96, [96, 96, 384, 192]),
+                                  (2, 192, 8, 128, 96, [96, 96, 384, 192]),
+                                  (1, 75, 32, 64, 25, [600, 75])],
+                         ids=["16x24grid", "64tok_frames", "8x12grid_96tok_frames", "8x12grid_96tok_D128",
+                              "audio_25tok_frames"])
 def test_flash_attn_fp8_kv(dev, case):
+    """fp8 K/V with one scale per (batch, head, frame); frames of 96 and 25
+    tokens are cut into 64-key tiles at frame boundaries (64 + 32, and one
+    partial tile per frame)."""
     B, Lq, H, D, frame, lens = case
     g = gen(9)
     q = randn((B, Lq, H, D), g, torch.bfloat16)
@@ -492,17 +499,18 @@ def test_flash_attn_fp8_kv(dev, case):
     assert_bf16_close(out, _ref_attn(q, Kd, Vd), "fp8 vs dequantised")
 
 
+@pytest.mark.parametrize("frame", [64, 96])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("scales", [(1, 1, 1, 1), (1, 6, 1, 12), (12, 1, 6, 1)], ids=["flat", "rising", "falling"])
-def test_flash_attn_fp8_ragged_segments(dev, D, scales):
+def test_flash_attn_fp8_ragged_segments(dev, D, scales, frame):
     """fp8 K/V in frame-aligned spans with gaps, segments ending mid-tile
     (partial last frames), per-frame scales spread over two orders of
     magnitude so later tiles raise the running maximum (rescale path).
     With scaled segments the softmax is so peaked that e4m3 rounding of K
     alone moves the fp32 answer (the oracle's own dequantised attention is at
     cosine 0.995 there), so those cases are held to the dequantised cache."""
-    B, Lq, H, frame = 2, 130, 2, 64
-    lens = [64, 100, 37, 192]
+    B, Lq, H = 2, 130, 2
+    lens = [64, 100, 37, 192] if frame == 64 else [96, 150, 37, 288]
     g = gen(13)
     q = randn((B, Lq, H, D), g, torch.bfloat16)
     ks = [randn((B, n, H, D), g, torch.bfloat16, scale=s) for n, s in zip(lens, scales)]

@@ -2,8 +2,9 @@
 attention layer, 8 heads x 64, 3-frame chunks, 12-frame window, 2 memory
 frames re-prefilled every 4 chunks) against the fp32 oracle replay of the same
 policy: every chunk's output, the final cache contents and the segment list.
-bf16 K/V on the 8x12 latent grid; fp8-e4m3 K/V on 8x16 (the fp8 kernel keeps
-one scale per 64-key tile, so a frame must hold a whole number of tiles)."""
+bf16 and fp8-e4m3 K/V on the 8x12 latent grid (96-token frames: the fp8
+kernel cuts its 64-key tiles at frame boundaries, 64 + 32 per frame), fp8
+also on 8x16 (128-token frames, two whole tiles)."""
 import pytest
 import torch
 
@@ -29,7 +30,8 @@ def _inputs_and_reference(w, grid):
     return xa, xm, chunks, OS.run_stream(w, grid, xa, xm, chunks)
 
 
-@pytest.mark.parametrize("kv_dtype,grid", [("bf16", (8, 12)), ("fp8", (8, 16))], ids=["bf16_8x12", "fp8_8x16"])
+@pytest.mark.parametrize("kv_dtype,grid", [("bf16", (8, 12)), ("fp8", (8, 12)), ("fp8", (8, 16))],
+                         ids=["bf16_8x12", "fp8_8x12", "fp8_8x16"])
 def test_chunk_stream_60_chunks(dev, kv_dtype, grid):
     attn, w = make_layer(dev, H * DH, H, DH, 50)
     if kv_dtype == "fp8":

@@ -77,6 +77,20 @@ def test_mask_preparation():
     assert RT.prepare_attention_mask(f, torch.bfloat16) is f
 
 
+def test_prepared_mask_kept_per_mask_tensor():
+    """The loop prepares a conditioning mask once: the same object while the
+    mask tensor is unchanged, a new one after an in-place change."""
+    gen = RT.StreamingGenerator(object(), (4, 6))
+    m = torch.tensor([[1, 1, 0, 0]])
+    a = gen._prepared_mask(m, torch.bfloat16)
+    assert gen._prepared_mask(m, torch.bfloat16) is a
+    torch.testing.assert_close(a, RT.prepare_attention_mask(m, torch.bfloat16))
+    m[0, 2] = 1
+    b = gen._prepared_mask(m, torch.bfloat16)
+    assert b is not a and b[0, 0, 0, 2].item() == 0.0
+    assert gen._prepared_mask(None, torch.bfloat16) is None
+
+
 def _cpu_kernels(monkeypatch):
     """Shape-correct stand-ins for the HIP entry points, so the loop's cache
     bookkeeping runs on the CPU (values are not checked here)."""

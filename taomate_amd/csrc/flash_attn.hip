@@ -858,20 +858,23 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
   };
   auto store_v8 = [&](int buf) {
     if (!fv_on) return;
-    uint4 v[4];
+    // The codes are interleaved by key before decoding: one v_perm puts
+    // channels c and c + 1 of keys 2i and 2i + 1 into one word, whose low and
+    // high byte pairs decode into the (key 2i, key 2i + 1) bf16 pairs of the
+    // two V^T rows.  8 perms and 16 decodes per thread, where decoding first
+    // and transposing the bf16 pairs takes 16 of each.
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = KVChunk<true>::to_bf16(vreg[e]);
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const uint32_t a0 = (&v[0].x)[w], a1 = (&v[1].x)[w], a2 = (&v[2].x)[w], a3 = (&v[3].x)[w];
-      // channels 8*chunk + 2w (low halves) and 2w + 1 (high halves) of keys 4*fvg .. +3
-      uint2 lo, hi;
-      lo.x = __builtin_amdgcn_perm(a1, a0, 0x05040100u);
-      lo.y = __builtin_amdgcn_perm(a3, a2, 0x05040100u);
-      hi.x = __builtin_amdgcn_perm(a1, a0, 0x07060302u);
-      hi.y = __builtin_amdgcn_perm(a3, a2, 0x07060302u);
-      *reinterpret_cast<uint2*>(&vbuf[buf][(fvc * 8 + 2 * w) * VS + fvg * 4]) = lo;
-      *reinterpret_cast<uint2*>(&vbuf[buf][(fvc * 8 + 2 * w + 1) * VS + fvg * 4]) = hi;
+    for (int half = 0; half < 2; ++half) {
+      const uint32_t d0 = half ? vreg[0].y : vreg[0].x, d1 = half ? vreg[1].y : vreg[1].x;
+      const uint32_t d2 = half ? vreg[2].y : vreg[2].x, d3 = half ? vreg[3].y : vreg[3].x;
+      // channels 4*half + {0, 1} and {2, 3} of keys (0, 1) and (2, 3)
+      const uint32_t k01a = __builtin_amdgcn_perm(d1, d0, 0x05010400u), k23a = __builtin_amdgcn_perm(d3, d2, 0x05010400u);
+      const uint32_t k01b = __builtin_amdgcn_perm(d1, d0, 0x07030602u), k23b = __builtin_amdgcn_perm(d3, d2, 0x07030602u);
+      uint16_t* row = &vbuf[buf][(fvc * 8 + 4 * half) * VS + fvg * 4];
+      *reinterpret_cast<uint2*>(row) = make_uint2(KVChunk<true>::pair(k01a, false), KVChunk<true>::pair(k23a, false));
+      *reinterpret_cast<uint2*>(row + VS) = make_uint2(KVChunk<true>::pair(k01a, true), KVChunk<true>::pair(k23a, true));
+      *reinterpret_cast<uint2*>(row + 2 * VS) = make_uint2(KVChunk<true>::pair(k01b, false), KVChunk<true>::pair(k23b, false));
+      *reinterpret_cast<uint2*>(row + 3 * VS) = make_uint2(KVChunk<true>::pair(k01b, true), KVChunk<true>::pair(k23b, true));
     }
   };
   // the tile the softmax works on: its valid keys and (fp8) its scales

@@ -851,31 +851,34 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
     }
     vit.next(p.v_ptr, v_head, v_tile, p);
   };
+  auto store_k8_row = [&](int buf, int i) {
+    *reinterpret_cast<uint4*>(&kbuf[buf][sig(fkr + FROWS * i) * KS + fkc * 8]) = KVChunk<true>::to_bf16(kreg[i]);
+  };
   auto store_k8 = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < FKL; ++i)
-      *reinterpret_cast<uint4*>(&kbuf[buf][sig(fkr + FROWS * i) * KS + fkc * 8]) = KVChunk<true>::to_bf16(kreg[i]);
+    for (int i = 0; i < FKL; ++i) store_k8_row(buf, i);
   };
-  auto store_v8 = [&](int buf) {
+  auto store_v8_half = [&](int buf, int half) {
     if (!fv_on) return;
-    // The codes are interleaved by key before decoding: one v_perm puts
-    // channels c and c + 1 of keys 2i and 2i + 1 into one word, whose low and
-    // high byte pairs decode into the (key 2i, key 2i + 1) bf16 pairs of the
-    // two V^T rows.  8 perms and 16 decodes per thread, where decoding first
-    // and transposing the bf16 pairs takes 16 of each.
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const uint32_t d0 = half ? vreg[0].y : vreg[0].x, d1 = half ? vreg[1].y : vreg[1].x;
-      const uint32_t d2 = half ? vreg[2].y : vreg[2].x, d3 = half ? vreg[3].y : vreg[3].x;
-      // channels 4*half + {0, 1} and {2, 3} of keys (0, 1) and (2, 3)
-      const uint32_t k01a = __builtin_amdgcn_perm(d1, d0, 0x05010400u), k23a = __builtin_amdgcn_perm(d3, d2, 0x05010400u);
-      const uint32_t k01b = __builtin_amdgcn_perm(d1, d0, 0x07030602u), k23b = __builtin_amdgcn_perm(d3, d2, 0x07030602u);
-      uint16_t* row = &vbuf[buf][(fvc * 8 + 4 * half) * VS + fvg * 4];
-      *reinterpret_cast<uint2*>(row) = make_uint2(KVChunk<true>::pair(k01a, false), KVChunk<true>::pair(k23a, false));
-      *reinterpret_cast<uint2*>(row + VS) = make_uint2(KVChunk<true>::pair(k01a, true), KVChunk<true>::pair(k23a, true));
-      *reinterpret_cast<uint2*>(row + 2 * VS) = make_uint2(KVChunk<true>::pair(k01b, false), KVChunk<true>::pair(k23b, false));
-      *reinterpret_cast<uint2*>(row + 3 * VS) = make_uint2(KVChunk<true>::pair(k01b, true), KVChunk<true>::pair(k23b, true));
-    }
+    const uint32_t d0 = half ? vreg[0].y : vreg[0].x, d1 = half ? vreg[1].y : vreg[1].x;
+    const uint32_t d2 = half ? vreg[2].y : vreg[2].x, d3 = half ? vreg[3].y : vreg[3].x;
+    // channels 4*half + {0, 1} and {2, 3} of keys (0, 1) and (2, 3)
+    const uint32_t k01a = __builtin_amdgcn_perm(d1, d0, 0x05010400u), k23a = __builtin_amdgcn_perm(d3, d2, 0x05010400u);
+    const uint32_t k01b = __builtin_amdgcn_perm(d1, d0, 0x07030602u), k23b = __builtin_amdgcn_perm(d3, d2, 0x07030602u);
+    uint16_t* row = &vbuf[buf][(fvc * 8 + 4 * half) * VS + fvg * 4];
+    *reinterpret_cast<uint2*>(row) = make_uint2(KVChunk<true>::pair(k01a, false), KVChunk<true>::pair(k23a, false));
+    *reinterpret_cast<uint2*>(row + VS) = make_uint2(KVChunk<true>::pair(k01a, true), KVChunk<true>::pair(k23a, true));
+    *reinterpret_cast<uint2*>(row + 2 * VS) = make_uint2(KVChunk<true>::pair(k01b, false), KVChunk<true>::pair(k23b, false));
+    *reinterpret_cast<uint2*>(row + 3 * VS) = make_uint2(KVChunk<true>::pair(k01b, true), KVChunk<true>::pair(k23b, true));
+  };
+  // V(j) to LDS: the codes are interleaved by key before decoding: one v_perm
+  // puts channels c and c + 1 of keys 2i and 2i + 1 into one word, whose low
+  // and high byte pairs decode into the (key 2i, key 2i + 1) bf16 pairs of the
+  // two V^T rows.  8 perms and 16 decodes per thread, where decoding first and
+  // transposing the bf16 pairs takes 16 of each.
+  auto store_v8 = [&](int buf) {
+    store_v8_half(buf, 0);
+    store_v8_half(buf, 1);
   };
   // the tile the softmax works on: its valid keys and (fp8) its scales
   KeyStreamT<FRAMED> cit;
@@ -987,10 +990,13 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
   // other VALU instructions of the same SIMD).
   constexpr int NS = 4 * DB + 2 * QS;
   constexpr int PREF = 3;
+  // fp8 staging inside the slot program: one unit (a K row chunk, a V half,
+  // a load) every kStageStride slots from kStageSlot0 on
+  constexpr int kStageSlot0 = 1, kStageStride = 2;
   const uint16_t* vf0 = &vbuf[0][li * VS + hg * 8];
   const uint16_t* kf0 = &kbuf[0][li * KS + hg * 8];
   auto tile = [&](int vb, int kbf, const f32x16_t (&scur)[2], f32x16_t (&snext)[2], const uint32_t (&pprev)[16],
-                  uint32_t (&pcur)[16], float& ps0, float& ps1, float c, float neg_m) {
+                  uint32_t (&pcur)[16], float& ps0, float& ps1, float c, float neg_m, auto&& slot_work) {
     const f32x16_t zero = f32x16_t{};
     const uint16_t* vf = vf0 + vb * VBUF;
     const uint16_t* kf = kf0 + kbf * KBUF;
@@ -1020,6 +1026,7 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
           snext[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], kk == 0 ? zero : snext[kb], 0, 0, 0);
         }
       }
+      slot_work(t);
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
         const int kb = q >> 3, r = (q & 7) * 2;
@@ -1097,11 +1104,7 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
       int nv;
       if constexpr (FP8) {
         // registers hold K(j+2) and V(j); LDS holds K(j+1) and V(j-1)
-        publish();                          // the buffers of K(j) and V(j-2) are free
-        if (j + 2 < ntiles) store_k8(j & 1);  // K(j+2)
-        store_v8(j & 1);                    // V(j)
-        if (j + 3 < ntiles) load_k8();      // K(j+3)
-        if (j + 1 < ntiles) load_v8();      // V(j+1)
+        publish();  // the buffers of K(j) and V(j-2) are free
         nv = cit.nvalid();
       } else {
         publish();  // K(j+1) and V(j-1) have landed; the buffers of K(j) and V(j-2) are free
@@ -1112,7 +1115,21 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
       if (nv < BN) mask_tail(scur, nv);
       const TileScale ts = tile_scale();
       float ps0, ps1;
-      tile((j - 1) & 1, (j + 1) & 1, scur, snext, pprev, pcur, ps0, ps1, ts.c, ts.off - m_run);
+      // fp8: the decode of K(j+2) and V(j) into the free buffers and the
+      // loads of K(j+3) and V(j+1) into the freed registers ride in the slot
+      // program, under the matrix work of tile j
+      tile((j - 1) & 1, (j + 1) & 1, scur, snext, pprev, pcur, ps0, ps1, ts.c, ts.off - m_run, [&](int t) {
+        if constexpr (FP8) {
+#pragma unroll
+          for (int i = 0; i < FKL; ++i)
+            if (t == kStageSlot0 + kStageStride * i && j + 2 < ntiles) store_k8_row(j & 1, i);  // K(j+2)
+          if (t == kStageSlot0 + kStageStride * FKL && j + 3 < ntiles) load_k8();               // K(j+3)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh)
+            if (t == kStageSlot0 + kStageStride * (FKL + 1 + hh)) store_v8_half(j & 1, hh);     // V(j)
+          if (t == kStageSlot0 + kStageStride * (FKL + 3) && j + 1 < ntiles) load_v8();         // V(j+1)
+        }
+      });
       float ps = (ps0 + ps1) * ts.inv;
       if (__builtin_amdgcn_ballot_w64(ps > kOver)) {
         // raise m to the tile maximum, rescale O and l, redo P(j) from S(j)

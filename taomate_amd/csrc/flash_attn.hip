@@ -611,9 +611,10 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // the same slot program (tiles cut at frame boundaries, see KeyStreamT).
 // Their tiles are staged through registers instead:
 // each thread loads 8-byte chunks of the next tiles from HBM one iteration
-// ahead, and after the barrier decodes them (exactly) to bf16 into the free
-// LDS buffers, K rows in the swapped order and V transposed with v_perm, so
-// every code is decoded once per workgroup.  A tile never crosses a frame
+// ahead, and decodes them (exactly) to bf16 into the LDS buffers the barrier
+// freed, K rows in the swapped order and V transposed with v_perm, so every
+// code is decoded once per workgroup.  The decode and the next loads are
+// spread over the slot program of the tile, under its matrix work.  A tile never crosses a frame
 // (KeyStreamT<true>), so its scales are two scalars: the K scale joins
 // the logit scale, c_j = c * sk_j, and the V scale joins the exponent,
 // P' = 2^(S c_j - m + log2 sv_j) = sv_j P, so the PV MFMAs read plain codes;

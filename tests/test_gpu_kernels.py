@@ -466,13 +466,18 @@ def test_flash_attn_key_mask(dev):
                                   (1, 192, 8, 64, 64, [128, 64, 384, 192]),
                                   (1, 192, 8, 64, 96, [96, 96, 384, 192]),
                                   (2, 192, 8, 128, 96, [96, 96, 384, 192]),
-                                  (1, 75, 32, 64, 25, [600, 75])],
+                                  (1, 75, 32, 64, 25, [600, 75]),
+                                  (1, 128, 4, 128, 64, [64]),
+                                  (1, 128, 4, 128, 64, [128]),
+                                  (1, 128, 4, 128, 64, [192]),
+                                  (2, 96, 4, 64, 64, [64, 64, 64])],
                          ids=["16x24grid", "64tok_frames", "8x12grid_96tok_frames", "8x12grid_96tok_D128",
-                              "audio_25tok_frames"])
+                              "audio_25tok_frames", "1_tile", "2_tiles", "3_tiles", "3_segments_of_1_tile"])
 def test_flash_attn_fp8_kv(dev, case):
     """fp8 K/V with one scale per (batch, head, frame); frames of 96 and 25
     tokens are cut into 64-key tiles at frame boundaries (64 + 32, and one
-    partial tile per frame)."""
+    partial tile per frame).  One to three key tiles exercise the staging
+    prologue and the last iterations of the tile loop."""
     B, Lq, H, D, frame, lens = case
     g = gen(9)
     q = randn((B, Lq, H, D), g, torch.bfloat16)

@@ -769,18 +769,13 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
   };
   // One load instruction ("slot" i of this wave) of a K or V tile.  rs is the
   // tile's buffer resource, l0 this wave's first LDS chunk of the buffer and
-  // nv the tile's valid keys (a segment's partial last tile re-reads its last
-  // row / 8-key chunk for the positions past its end).
-  auto k_load = [&](__amdgpu_buffer_rsrc_t rs, uint32_t l0, int nv, int i) {
-    if (i < KSLOT && wave + 4 * i < KINS) {
-      int off = koff[i];
-      if (nv < BN) {
-        int r, c;
-        kpos(i, r, c);
-        off = min(r, nv - 1) * row_bytes + c * 16;
-      }
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(uintptr_t)(l0 + i * 4096), 16, off, 0, 0, 0);
-    }
+  // nv the tile's valid keys.  K rows past a segment's end lie outside the
+  // partial tile's buffer range (issue_k): those lanes load zeros, and their
+  // scores are masked out of the softmax.  V (8-key chunks of key-major rows)
+  // re-reads the segment's last chunk for the positions past its end.
+  auto k_load = [&](__amdgpu_buffer_rsrc_t rs, uint32_t l0, int i) {
+    if (i < KSLOT && wave + 4 * i < KINS)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(uintptr_t)(l0 + i * 4096), 16, koff[i], 0, 0, 0);
   };
   auto v_load = [&](__amdgpu_buffer_rsrc_t rs, uint32_t l0, int nv, int i) {
     if (i < VSLOT && wave + 4 * i < VINS) {
@@ -795,18 +790,16 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
   };
   auto rsrc = [&](const char* ptr) { return __builtin_amdgcn_make_buffer_rsrc((void*)ptr, (short)0, 0x7FFFFFFF, 0x00020000); };
   // whole tiles (every tile but a segment's last) take one branch and issue
-  // their loads from the precomputed offsets
+  // their loads from the precomputed offsets; a K tile's buffer range ends at
+  // its last valid row (a whole tile's is left open), so the partial tile
+  // issues the same loads
   auto issue_k = [&](int buf) {
-    const auto rs = rsrc(kit.ptr);
-    const uint32_t l0 = lds_slot0(kbuf[buf]);
     const int nv = kit.nvalid();
-    if (nv == BN) {
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc((void*)kit.ptr, (short)0, nv == BN ? 0x7FFFFFFF : nv * row_bytes,
+                                                      0x00020000);
+    const uint32_t l0 = lds_slot0(kbuf[buf]);
 #pragma unroll
-      for (int i = 0; i < KSLOT; ++i) k_load(rs, l0, BN, i);
-    } else {
-#pragma unroll
-      for (int i = 0; i < KSLOT; ++i) k_load(rs, l0, nv, i);
-    }
+    for (int i = 0; i < KSLOT; ++i) k_load(rs, l0, i);
     kit.next(p.k_ptr, k_head, k_tile, p);
   };
   auto issue_v = [&](int buf) {
@@ -985,12 +978,17 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
   // (2*QS MFMAs over kbuf[kbf]).  Each slot issues its MFMA, the LDS read
   // of the fragment PREF slots ahead, and a slice of the softmax of S(j):
   // score pair p (of 16 per lane) has its fma at slot 2p*NS/32, its exp one
-  // step later and its bf16 pack + row-sum dot2 two steps after that.  A
+  // step later and its bf16 pack + row-sum adds two steps after that.  A
   // scheduling fence closes every slot, so the exp work stays spread under
   // the MFMAs (each 32x32x16 MFMA leaves room for about two exp and two
-  // other VALU instructions of the same SIMD).
+  // other VALU instructions of the same SIMD).  The row sum adds the fp32 P
+  // values: v_dot2c_f32_bf16 over the packed pair (one instruction instead
+  // of two) waits for the SIMD's matrix pipeline on gfx950, about one MFMA
+  // per instruction while the other wave's MFMAs run, where adds issue
+  // beside them (bf16 instances; fp8 keeps the dot2).  Two fragment reads
+  // ahead keep the bf16 D = 128 instance at 256 VGPRs with no spills.
   constexpr int NS = 4 * DB + 2 * QS;
-  constexpr int PREF = 3;
+  constexpr int PREF = FP8 ? 3 : 2;
   // fp8 staging inside the slot program: one unit (a K row chunk, a V half,
   // a load) every kStageStride slots from kStageSlot0 on
   constexpr int kStageSlot0 = 1, kStageStride = 2;
@@ -1042,7 +1040,14 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
         if ((2 * q * NS) / 32 + 3 == t || (q == 15 && t == NS + 1 && (2 * q * NS) / 32 + 3 > NS + 1)) {
           pcur[q] = pack_bf16x2(e0[q], e1[q]);
           float& ps = (q & 1) ? ps1 : ps0;
-          ps = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(ltx_bf16x2_t, pcur[q]), ones, ps, false);
+          if constexpr (FP8) {
+            // the fp8 instances keep the packed dot2 (their staging
+            // registers leave no room for the adds' live ranges)
+            ps = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(ltx_bf16x2_t, pcur[q]), ones, ps, false);
+          } else {
+            ps = ps + e0[q];
+            ps = ps + e1[q];
+          }
         }
       }
       __builtin_amdgcn_sched_barrier(0);

@@ -985,10 +985,9 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
   // values: v_dot2c_f32_bf16 over the packed pair (one instruction instead
   // of two) waits for the SIMD's matrix pipeline on gfx950, about one MFMA
   // per instruction while the other wave's MFMAs run, where adds issue
-  // beside them (bf16 instances; fp8 keeps the dot2).  Two fragment reads
-  // ahead keep the bf16 D = 128 instance at 256 VGPRs with no spills.
+  // beside them (bf16 instances; fp8 keeps the dot2).
   constexpr int NS = 4 * DB + 2 * QS;
-  constexpr int PREF = FP8 ? 3 : 2;
+  constexpr int PREF = 3;
   // fp8 staging inside the slot program: one unit (a K row chunk, a V half,
   // a load) every kStageStride slots from kStageSlot0 on
   constexpr int kStageSlot0 = 1, kStageStride = 2;
@@ -1047,6 +1046,10 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
           } else {
             ps = ps + e0[q];
             ps = ps + e1[q];
+            // with no use left in this slot the compiler would sink the pack
+            // to the next tile's PV and issue all sixteen back to back after
+            // the slot program; pin it here, under this slot's MFMA
+            asm volatile("" : "+v"(pcur[q]));
           }
         }
       }

@@ -63,6 +63,10 @@ struct FlashParams {
   // q-tiles is cut into `split` key ranges run by separate workgroups, whose
   // partial results meet in the workspace and are combined by a second kernel.
   int n_full, split;
+  // pair kernel (bf16 key-major V, n_qtiles even): work unit u is q-tiles 2u
+  // and 2u + 1, which lie in one (batch, head) and share every K/V tile;
+  // n_full and split count units, and the tail q-tiles start at 2 n_full.
+  int pair;
   uint16_t* part_o;  // [tail tiles * split][kBM][D] bf16 O / l of the key range (0 where l = 0)
   float* part_ml;     // [tail tiles * split][kBM][2] running max (log2) and sum
   float scale;       // softmax scale applied to q.k
@@ -206,6 +210,32 @@ __device__ __forceinline__ WorkItem work_item(const FlashParams& p, int bid, int
   return w;
 }
 
+// Work of group grp of pair workgroup `bid`: q-tile 2u + grp of unit u
+// (units below n_full run whole, the rest 1/split of their key tiles; a
+// split unit's two q-tiles are tail q-tiles 2 tu and 2 tu + 1).
+__device__ __forceinline__ WorkItem pair_work(const FlashParams& p, int bid, int grp, int ntiles) {
+  WorkItem w;
+  int u;
+  if (bid < p.n_full) {
+    u = xcd_remap(bid, p.n_full);
+    w.j0 = 0;
+    w.j1 = ntiles;
+    w.piece = -1;
+    w.tail = -1;
+  } else {
+    const int ntail = gridDim.x - p.n_full;
+    const int t = xcd_remap(bid - p.n_full, ntail);
+    const int tu = t / p.split, part = t % p.split;
+    u = p.n_full + tu;
+    w.j0 = (int)((int64_t)ntiles * part / p.split);
+    w.j1 = (int)((int64_t)ntiles * (part + 1) / p.split);
+    w.tail = 2 * tu + grp;
+    w.piece = w.tail * p.split + part;
+  }
+  w.qtile = 2 * u + grp;
+  return w;
+}
+
 // Epilogue shared by the kernels: normalise and store a whole q-tile, or
 // store a key range's partial result (unnormalised O, running max and sum).  oacc holds O^T fragments (lane: query li,
 // d = db*32 + 8*(r/4) + 4*hg + r%4); m_run / l_tot are per query.
@@ -274,7 +304,7 @@ __global__ void __launch_bounds__(256) flash_combine_kernel(const FlashParams p)
   const int tail = blockIdx.x / WG_PER_TILE;
   const int r = (blockIdx.x % WG_PER_TILE) * ROWS + threadIdx.x / CG;
   const int cg = threadIdx.x % CG;
-  const int qtile = p.n_full + tail;
+  const int qtile = (p.pair ? 2 * p.n_full : p.n_full) + tail;
   const int qt = qtile % p.n_qtiles;
   const int bh = qtile / p.n_qtiles;
   const int b = bh / p.H, h = bh % p.H;
@@ -691,9 +721,19 @@ struct KeyStreamT {
 // crosses a frame either and keeps the hot kernel's scalar state and
 // registers as they were (the framed state costs the D = 128 instance
 // register spills).
-template <int D, bool FP8, bool FRAMED>
+//
+// PAIR (bf16): 8-wave workgroups of two groups of 4 waves (waves w and w + 4
+// share a SIMD) that own two q-tiles of one head (pair_work) and read one
+// K/V stream.  Only group 0 issues the tile loads, so group 1's waves run
+// their slot programs while group 0's wait on the load pipe, and the groups
+// meet at every per-tile barrier: the two waves of a SIMD finish together,
+// where two 4-wave workgroups on one CU do not (the older one's waves win
+// the issue arbitration and finish about a quarter earlier, leaving the CU
+// half busy until the other ends).
+template <int D, bool FP8, bool FRAMED, bool PAIR = false>
 __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
   static_assert(FP8 || !FRAMED, "frame tiling is an fp8 feature");
+  static_assert(!(PAIR && FP8), "pair workgroups are a bf16 feature");
   constexpr int BM = kBM, BN = kBN;
   constexpr int NKC = D / 8;
   constexpr int KS = D + 8;
@@ -712,7 +752,10 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
   __shared__ __attribute__((aligned(16))) uint16_t kbuf[2][KBUF];
   __shared__ __attribute__((aligned(16))) uint16_t vbuf[2][VBUF];
 
-  const WorkItem wi = work_item(p, blockIdx.x, p.tile_start[p.n_seg]);
+  const int grp = PAIR ? (__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) >> 2) : 0;
+  const WorkItem wi = PAIR ? pair_work(p, blockIdx.x, grp, p.tile_start[p.n_seg])
+                           : work_item(p, blockIdx.x, p.tile_start[p.n_seg]);
+  const bool loader = !PAIR || grp == 0;  // issues the K/V tile loads
   const int qt = wi.qtile % p.n_qtiles;
   const int bh = wi.qtile / p.n_qtiles;
   const int b = bh / p.H, h = bh % p.H;
@@ -774,11 +817,11 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
   // scores are masked out of the softmax.  V (8-key chunks of key-major rows)
   // re-reads the segment's last chunk for the positions past its end.
   auto k_load = [&](__amdgpu_buffer_rsrc_t rs, uint32_t l0, int i) {
-    if (i < KSLOT && wave + 4 * i < KINS)
+    if (loader && i < KSLOT && wave + 4 * i < KINS)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(uintptr_t)(l0 + i * 4096), 16, koff[i], 0, 0, 0);
   };
   auto v_load = [&](__amdgpu_buffer_rsrc_t rs, uint32_t l0, int nv, int i) {
-    if (i < VSLOT && wave + 4 * i < VINS) {
+    if (loader && i < VSLOT && wave + 4 * i < VINS) {
       int off = voff[i];
       if (nv < BN) {
         int d, c;
@@ -1167,13 +1210,19 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
       pv_tile(0, pa);
   }
 
-  finish_tile<D>(p, wi, b, h, qt, (int)(threadIdx.x >> 6) * 32 + (int)(threadIdx.x & 31), oacc, m_run,
-                 pair_sum(l_run));
+  finish_tile<D>(p, wi, b, h, qt, (PAIR ? wave : (int)(threadIdx.x >> 6)) * 32 + (int)(threadIdx.x & 31), oacc,
+                 m_run, pair_sum(l_run));
 }
 
 template <int D, bool FP8>
 __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParams p) {
   flash_pipe_body<D, FP8, false>(p);
+}
+
+// bf16 key-major V with an even number of q-tiles per head: pair workgroups
+template <int D>
+__global__ void __launch_bounds__(512, 1) flash_fwd_pair_kernel(const FlashParams p) {
+  flash_pipe_body<D, false, false, true>(p);
 }
 
 // fp8 frames that are not a whole number of 64-key tiles
@@ -1185,16 +1234,17 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_framed_kernel(const Fla
 template <int D>
 int launch_combine(const FlashParams& p, hipStream_t st) {
   if (p.split <= 1) return LTX_OK;
-  const int64_t tail = (int64_t)p.B * p.H * p.n_qtiles - p.n_full;
+  const int64_t tail = (int64_t)p.B * p.H * p.n_qtiles - (p.pair ? 2 * (int64_t)p.n_full : p.n_full);
   const int64_t wg_per_tile = combine_wg_per_tile<D>();
   hipLaunchKernelGGL((flash_combine_kernel<D>), dim3((unsigned)(tail * wg_per_tile)), dim3(256), 0, st, p);
   LTX_LAUNCH_CHECK("ltx_flash_attn_fwd (combine)");
   return LTX_OK;
 }
 
-// Grid: whole q-tiles first, then the key-range pieces of the tail q-tiles.
+// Grid: whole q-tiles (pair kernel: units of two) first, then the key-range
+// pieces of the tail ones.
 inline int64_t grid_blocks(const FlashParams& p) {
-  const int64_t nq = (int64_t)p.B * p.H * p.n_qtiles;
+  const int64_t nq = (int64_t)p.B * p.H * p.n_qtiles / (p.pair ? 2 : 1);
   return p.n_full + (nq - p.n_full) * p.split;
 }
 
@@ -1205,6 +1255,8 @@ int launch_flash_pipe(const FlashParams& p, hipStream_t st) {
   LTX_REQUIRE(nblocks <= 0x7FFFFFFF, "ltx_flash_attn_fwd: grid too large");
   if constexpr (FRAMED)
     hipLaunchKernelGGL((flash_fwd_pipe_framed_kernel<D>), dim3((unsigned)nblocks), dim3(256), 0, st, p);
+  else if (!FP8 && p.pair)
+    hipLaunchKernelGGL((flash_fwd_pair_kernel<D>), dim3((unsigned)nblocks), dim3(512), 0, st, p);
   else
     hipLaunchKernelGGL((flash_fwd_pipe_kernel<D, FP8>), dim3((unsigned)nblocks), dim3(256), 0, st, p);
   LTX_LAUNCH_CHECK("ltx_flash_attn_fwd");
@@ -1229,37 +1281,50 @@ using namespace ltx;
 // threads may race to fill it); one table per kernel (each instantiation of
 // the template has its own).
 constexpr int kMaxDevices = 64;
+struct Slots {
+  int slots;   // resident workgroups (0: unknown, no split is planned)
+  int per_cu;  // of them on one CU
+};
 template <auto Kernel>
-int resident_slots(int threads = 256) {
+Slots resident_slots(int threads = 256) {
   static std::once_flag once[kMaxDevices];
-  static int slots[kMaxDevices];
+  static Slots slots[kMaxDevices];
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return Slots{0, 1};
   std::call_once(once[dev], [&]() {
     int cus = 0, occ = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, Kernel, threads, 0) != hipSuccess) {
-      slots[dev] = 0;  // no split is planned on this device
+      slots[dev] = Slots{0, 1};
       return;
     }
-    slots[dev] = cus * (occ > 0 ? occ : 1);
+    occ = occ > 0 ? occ : 1;
+    slots[dev] = Slots{cus * occ, occ};
   });
   return slots[dev];
 }
 
 // Tail q-tiles (those past the last whole round of resident slots) and how
-// many key ranges each is cut into: enough pieces to fill the resident slots
-// once more, so the last round drains together with no idle slots.  Only
-// worth it when there is at least one whole round (otherwise the grid is a
-// single partial round and the extra combine launch costs more than it
-// saves) and each piece keeps >= 4 key tiles.  Zero tail tiles: no split.
-inline void plan_split(int64_t nq, int ntiles, int slots, int64_t* n_full, int* split) {
+// many key ranges each is cut into: about one piece per CU.  Of the
+// workgroups one CU holds, the oldest one's waves win the issue arbitration:
+// with two 4-wave workgroups per CU the older finishes its q-tile about a
+// quarter before the younger, so one slot per CU frees early.  Pieces that
+// fill just those slots run beside the younger workgroups' last stretch;
+// pieces for every slot (twice as many, half as long) leave their second
+// half to start only when the younger workgroups end, with a CU half busy
+// until they drain (193.7 against 184.8 us for the bf16 step at 1152 x 4608,
+// 8 against 4 pieces per tail q-tile).  Only worth it when there is at
+// least one whole round (otherwise the grid is a single partial round and
+// the extra combine launch costs more than it saves) and each piece keeps
+// >= 4 key tiles.  Zero tail tiles: no split.
+inline void plan_split(int64_t nq, int ntiles, Slots s, int64_t* n_full, int* split) {
   *n_full = nq;
   *split = 1;
+  const int slots = s.slots;
   if (slots <= 0 || nq < slots || nq % slots == 0) return;
   const int64_t full = (nq / slots) * slots;
   const int64_t tail = nq - full;
-  int sp = (int)(slots / tail);
+  int sp = (int)((slots / s.per_cu) / tail);
   if (sp > kMaxSplit) sp = kMaxSplit;
   if (sp > ntiles / 4) sp = ntiles / 4;
   if (sp < 2) return;
@@ -1271,19 +1336,22 @@ inline int64_t workspace_bytes_for(int64_t tail, int split, int64_t D) {
   return tail * split * kBM * (2 * 4 + D * 2);  // (max, sum) fp32 + bf16 O row
 }
 
-// Resident slots of the kernel a call with head size D takes: the pipelined
-// kernel for key-major bf16 V (vkey) or fp8 K/V, else the staged kernel
-// (its masked instance for a key mask).
-inline int flash_slots(int64_t D, bool vkey, bool fp8, bool mask) {
+// Resident slots of the kernel a call with head size D takes: for
+// key-major bf16 V (vkey) the pair kernel when the q-tiles per head are
+// even (pair), else the pipelined kernel; the pipelined kernel for fp8 K/V;
+// else the staged kernel (its masked instance for a key mask).
+inline Slots flash_slots(int64_t D, bool vkey, bool fp8, bool mask, bool pair) {
   if (D == 128)
-    return vkey   ? resident_slots<flash_fwd_pipe_kernel<128, false>>()
-           : fp8  ? resident_slots<flash_fwd_pipe_kernel<128, true>>()
-           : mask ? resident_slots<flash_fwd_kernel<128, false, true>>()
-                  : resident_slots<flash_fwd_kernel<128, false, false>>();
-  return vkey   ? resident_slots<flash_fwd_pipe_kernel<64, false>>()
-         : fp8  ? resident_slots<flash_fwd_pipe_kernel<64, true>>()
-         : mask ? resident_slots<flash_fwd_kernel<64, false, true>>()
-                : resident_slots<flash_fwd_kernel<64, false, false>>();
+    return vkey && pair ? resident_slots<flash_fwd_pair_kernel<128>>(512)
+           : vkey       ? resident_slots<flash_fwd_pipe_kernel<128, false>>()
+           : fp8        ? resident_slots<flash_fwd_pipe_kernel<128, true>>()
+           : mask       ? resident_slots<flash_fwd_kernel<128, false, true>>()
+                        : resident_slots<flash_fwd_kernel<128, false, false>>();
+  return vkey && pair ? resident_slots<flash_fwd_pair_kernel<64>>(512)
+         : vkey       ? resident_slots<flash_fwd_pipe_kernel<64, false>>()
+         : fp8        ? resident_slots<flash_fwd_pipe_kernel<64, true>>()
+         : mask       ? resident_slots<flash_fwd_kernel<64, false, true>>()
+                      : resident_slots<flash_fwd_kernel<64, false, false>>();
 }
 
 extern "C" int ltx_flash_attn_workspace_size(int64_t B, int64_t Lq, int64_t H, int64_t D,
@@ -1291,15 +1359,19 @@ extern "C" int ltx_flash_attn_workspace_size(int64_t B, int64_t Lq, int64_t H, i
   clear_error();
   LTX_REQUIRE(bytes != nullptr && B >= 1 && H >= 1 && Lq >= 0 && (D == 64 || D == 128),
               "ltx_flash_attn_workspace_size: bad arguments");
-  // the largest partial buffer any of the kernels for this D may plan
-  const int64_t nq = B * H * ((Lq + kBM - 1) / kBM);
+  // the largest partial buffer any of the kernels for this D may plan (the
+  // pair kernel plans over units of two q-tiles)
+  const int64_t nqt = (Lq + kBM - 1) / kBM;
+  const int64_t nq = B * H * nqt;
+  const bool pair = nqt % 2 == 0;
   int64_t need = 0;
   for (int k = 0; k < 4; ++k) {
-    const int slots = flash_slots(D, k == 1, k == 2, k == 3);
+    const bool kp = k == 1 && pair;
+    const int64_t nu = kp ? nq / 2 : nq;
     int64_t n_full;
     int split;
-    plan_split(nq, 1 << 30, slots, &n_full, &split);
-    const int64_t b = split > 1 ? workspace_bytes_for(nq - n_full, kMaxSplit, D) : 0;
+    plan_split(nu, 1 << 30, flash_slots(D, k == 1, k == 2, k == 3, pair), &n_full, &split);
+    const int64_t b = split > 1 ? workspace_bytes_for((nu - n_full) * (kp ? 2 : 1), kMaxSplit, D) : 0;
     need = b > need ? b : need;
   }
   *bytes = need;
@@ -1405,21 +1477,27 @@ static int flash_attn_fwd_impl(const void* q, int64_t B, int64_t Lq, int64_t H, 
   if (Lq == 0) return LTX_OK;
   LTX_REQUIRE(n > 0, "ltx_flash_attn_fwd: no keys (Lk == 0)");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  // balanced tail (needs a workspace; without one every q-tile runs whole)
+  // balanced tail (needs a workspace; without one every q-tile runs whole).
+  // Key-major bf16 V with an even number of q-tiles per head runs the pair
+  // kernel, whose grid counts units of two q-tiles (two partial results per
+  // split unit).
   {
     const int64_t nq = (int64_t)B * H * p.n_qtiles;
     LTX_REQUIRE(nq <= 0x7FFFFFFF, "ltx_flash_attn_fwd: grid too large");
-    int64_t n_full = nq;
+    p.pair = vkey && p.n_qtiles % 2 == 0 ? 1 : 0;
+    const int64_t nu = p.pair ? nq / 2 : nq;
+    const int per_unit = p.pair ? 2 : 1;
+    int64_t n_full = nu;
     int split = 1;
     if (workspace != nullptr) {
-      const int slots = flash_slots(D, vkey, fp8, key_mask != nullptr);
-      plan_split(nq, p.tile_start[n], slots, &n_full, &split);
-      if (split > 1 && workspace_bytes_for(nq - n_full, split, D) > workspace_bytes) {
+      plan_split(nu, p.tile_start[n], flash_slots(D, vkey, fp8, key_mask != nullptr, p.pair != 0), &n_full,
+                 &split);
+      if (split > 1 && workspace_bytes_for((nu - n_full) * per_unit, split, D) > workspace_bytes) {
         LTX_REQUIRE(!strict_ws,
                     "ltx_flash_attn_fwd_noalloc: this call's split partials need %lld bytes, more than the "
                     "%lld-byte scratch array",
-                    (long long)workspace_bytes_for(nq - n_full, split, D), (long long)workspace_bytes);
-        n_full = nq;
+                    (long long)workspace_bytes_for((nu - n_full) * per_unit, split, D), (long long)workspace_bytes);
+        n_full = nu;
         split = 1;
       }
     }
@@ -1427,7 +1505,7 @@ static int flash_attn_fwd_impl(const void* q, int64_t B, int64_t Lq, int64_t H, 
     p.split = split;
     if (split > 1) {
       LTX_REQUIRE(al(workspace, 256), "ltx_flash_attn_fwd: workspace must be 256-byte aligned");
-      const int64_t tail = nq - n_full;
+      const int64_t tail = (nu - n_full) * per_unit;
       p.part_ml = static_cast<float*>(workspace);
       p.part_o = reinterpret_cast<uint16_t*>(p.part_ml + tail * split * kBM * 2);
     }
@@ -1476,10 +1554,10 @@ extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t 
 // No-allocation variant: the split partials live in a fixed device array.
 //
 // `scratch` holds the partial results of the split tail q-tiles (per piece:
-// 128 rows of (max, sum) in float32 and an O row in bf16).  The pieces of a
-// tail q-tile are at most the device's resident workgroups (tail x split <=
-// slots), so a call needs at most slots x 128 x (8 + 2 D) bytes: 17.3 MB for
-// D = 128 at 512 slots.  Every piece writes its whole partial before the
+// 128 rows of (max, sum) in float32 and an O row in bf16).  The pieces are
+// at most one per CU (tail x split <= CUs; the pair kernel's units hold two
+// q-tiles, so 2 CUs there), so a call needs at most 2 CUs x 128 x (8 + 2 D)
+// bytes: 17.3 MB for D = 128 at 256 CUs.  Every piece writes its whole partial before the
 // combine kernel reads it, so nothing needs clearing between calls.  Each
 // device holds its own copy of the array for the life of the process; its
 // device address is looked up once per device (hipGetSymbolAddress) and

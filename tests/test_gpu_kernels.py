@@ -582,12 +582,14 @@ def test_adaln_matches_torch_ops(dev, C, L, per_row):
 
 
 @pytest.mark.parametrize("vlayout", ["token", "key"])
-def test_flash_attn_d64_split_tail(dev, vlayout):
-    """D = 64 with enough q-tiles to leave a partial last round (B=2, H=64,
-    1152 queries = 1152 q-tiles) and 32 key tiles, so the tail q-tiles are cut
-    into key ranges and merged by the D = 64 combine kernel; both V layouts
-    against fp32."""
-    B, Lq, H, D, lens = 2, 1152, 64, 64, [1024, 1024]
+@pytest.mark.parametrize("D,Lq,H", [(64, 1152, 64), (64, 1280, 64), (128, 1280, 32)])
+def test_flash_attn_split_tail(dev, vlayout, D, Lq, H):
+    """Enough q-tiles to leave a partial last round and 32 key tiles, so the
+    tail q-tiles are cut into key ranges and merged by the combine kernel;
+    both V layouts against fp32.  1152 queries (9 q-tiles per head) run the
+    4-wave kernels; 1280 (10 per head) with key-major V runs the pair kernel,
+    whose split units each leave two q-tiles' partials."""
+    B, lens = 2, [1024, 1024]
     ws = ctypes.c_int64(0)
     _native.call("ltx_flash_attn_workspace_size", B, Lq, H, D, ctypes.byref(ws))
     assert ws.value > 0, "the shape must plan a split tail"
@@ -609,4 +611,4 @@ def test_flash_attn_d64_split_tail(dev, vlayout):
     out = torch.empty(B, Lq, H, D, dtype=torch.bfloat16, device=dev)
     kernels.flash_attn(q.to(dev), segs, out)
     torch.cuda.synchronize()
-    assert_bf16_close(out, _ref_attn(q, torch.cat(ks, 1), torch.cat(vs, 1)), f"D64 split tail {vlayout}")
+    assert_bf16_close(out, _ref_attn(q, torch.cat(ks, 1), torch.cat(vs, 1)), f"D{D} Lq{Lq} split tail {vlayout}")

@@ -1283,7 +1283,7 @@ using namespace ltx;
 constexpr int kMaxDevices = 64;
 struct Slots {
   int slots;   // resident workgroups (0: unknown, no split is planned)
-  int per_cu;  // of them on one CU
+  int pieces;  // key-range pieces a split tail aims for (see plan_split)
 };
 template <auto Kernel>
 Slots resident_slots(int threads = 256) {
@@ -1299,24 +1299,27 @@ Slots resident_slots(int threads = 256) {
       return;
     }
     occ = occ > 0 ? occ : 1;
-    slots[dev] = Slots{cus * occ, occ};
+    slots[dev] = Slots{cus * occ, cus};  // pieces: one per CU until flash_slots says otherwise
   });
   return slots[dev];
 }
 
 // Tail q-tiles (those past the last whole round of resident slots) and how
-// many key ranges each is cut into: about one piece per CU.  Of the
-// workgroups one CU holds, the oldest one's waves win the issue arbitration:
-// with two 4-wave workgroups per CU the older finishes its q-tile about a
-// quarter before the younger, so one slot per CU frees early.  Pieces that
-// fill just those slots run beside the younger workgroups' last stretch;
-// pieces for every slot (twice as many, half as long) leave their second
-// half to start only when the younger workgroups end, with a CU half busy
-// until they drain (193.7 against 184.8 us for the bf16 step at 1152 x 4608,
-// 8 against 4 pieces per tail q-tile).  Only worth it when there is at
-// least one whole round (otherwise the grid is a single partial round and
-// the extra combine launch costs more than it saves) and each piece keeps
-// >= 4 key tiles.  Zero tail tiles: no split.
+// many key ranges each is cut into: about s.pieces pieces in all.  For the
+// bf16 pipelined kernel that is one per CU.  Of the workgroups one CU holds,
+// the oldest one's waves win the issue arbitration: with two of its 4-wave
+// workgroups per CU the older finishes its q-tile about a quarter before the
+// younger, so one slot per CU frees early.  Pieces that fill just those
+// slots run beside the younger workgroups' last stretch; pieces for every
+// slot (twice as many, half as long) leave their second half to start only
+// when the younger workgroups end, with a CU half busy until they drain
+// (193.7 against 184.8 us for the bf16 step at 1152 x 4608, 8 against 4
+// pieces per tail q-tile).  The fp8 kernel is the other way round (194-196
+// against 200-202 us), so its pieces fill every slot, as do the staged
+// kernel's.  Only worth it when there is at least one whole round
+// (otherwise the grid is a single partial round and the extra combine
+// launch costs more than it saves) and each piece keeps >= 4 key tiles.
+// Zero tail tiles: no split.
 inline void plan_split(int64_t nq, int ntiles, Slots s, int64_t* n_full, int* split) {
   *n_full = nq;
   *split = 1;
@@ -1324,7 +1327,7 @@ inline void plan_split(int64_t nq, int ntiles, Slots s, int64_t* n_full, int* sp
   if (slots <= 0 || nq < slots || nq % slots == 0) return;
   const int64_t full = (nq / slots) * slots;
   const int64_t tail = nq - full;
-  int sp = (int)((slots / s.per_cu) / tail);
+  int sp = (int)(s.pieces / tail);
   if (sp > kMaxSplit) sp = kMaxSplit;
   if (sp > ntiles / 4) sp = ntiles / 4;
   if (sp < 2) return;
@@ -1341,17 +1344,23 @@ inline int64_t workspace_bytes_for(int64_t tail, int split, int64_t D) {
 // even (pair), else the pipelined kernel; the pipelined kernel for fp8 K/V;
 // else the staged kernel (its masked instance for a key mask).
 inline Slots flash_slots(int64_t D, bool vkey, bool fp8, bool mask, bool pair) {
+  Slots s;
   if (D == 128)
-    return vkey && pair ? resident_slots<flash_fwd_pair_kernel<128>>(512)
-           : vkey       ? resident_slots<flash_fwd_pipe_kernel<128, false>>()
-           : fp8        ? resident_slots<flash_fwd_pipe_kernel<128, true>>()
-           : mask       ? resident_slots<flash_fwd_kernel<128, false, true>>()
-                        : resident_slots<flash_fwd_kernel<128, false, false>>();
-  return vkey && pair ? resident_slots<flash_fwd_pair_kernel<64>>(512)
-         : vkey       ? resident_slots<flash_fwd_pipe_kernel<64, false>>()
-         : fp8        ? resident_slots<flash_fwd_pipe_kernel<64, true>>()
-         : mask       ? resident_slots<flash_fwd_kernel<64, false, true>>()
-                      : resident_slots<flash_fwd_kernel<64, false, false>>();
+    s = vkey && pair ? resident_slots<flash_fwd_pair_kernel<128>>(512)
+        : vkey       ? resident_slots<flash_fwd_pipe_kernel<128, false>>()
+        : fp8        ? resident_slots<flash_fwd_pipe_kernel<128, true>>()
+        : mask       ? resident_slots<flash_fwd_kernel<128, false, true>>()
+                     : resident_slots<flash_fwd_kernel<128, false, false>>();
+  else
+    s = vkey && pair ? resident_slots<flash_fwd_pair_kernel<64>>(512)
+        : vkey       ? resident_slots<flash_fwd_pipe_kernel<64, false>>()
+        : fp8        ? resident_slots<flash_fwd_pipe_kernel<64, true>>()
+        : mask       ? resident_slots<flash_fwd_kernel<64, false, true>>()
+                     : resident_slots<flash_fwd_kernel<64, false, false>>();
+  // pieces: one per CU for the bf16 pipelined kernel (and the pair kernel,
+  // one workgroup per CU), one per slot for the others (plan_split)
+  if (!vkey) s.pieces = s.slots;
+  return s;
 }
 
 extern "C" int ltx_flash_attn_workspace_size(int64_t B, int64_t Lq, int64_t H, int64_t D,
@@ -1554,10 +1563,11 @@ extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t 
 // No-allocation variant: the split partials live in a fixed device array.
 //
 // `scratch` holds the partial results of the split tail q-tiles (per piece:
-// 128 rows of (max, sum) in float32 and an O row in bf16).  The pieces are
-// at most one per CU (tail x split <= CUs; the pair kernel's units hold two
-// q-tiles, so 2 CUs there), so a call needs at most 2 CUs x 128 x (8 + 2 D)
-// bytes: 17.3 MB for D = 128 at 256 CUs.  Every piece writes its whole partial before the
+// 128 rows of (max, sum) in float32 and an O row in bf16).  The partial
+// results are at most two per CU (pieces <= resident slots, two 4-wave
+// workgroups per CU; the pair kernel's units hold two q-tiles at one
+// workgroup per CU), so a call needs at most 2 CUs x 128 x (8 + 2 D) bytes:
+// 17.3 MB for D = 128 at 256 CUs.  Every piece writes its whole partial before the
 // combine kernel reads it, so nothing needs clearing between calls.  Each
 // device holds its own copy of the array for the life of the process; its
 // device address is looked up once per device (hipGetSymbolAddress) and

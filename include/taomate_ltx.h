@@ -235,9 +235,9 @@ int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t H, int64_t 
  *   LTX_NOALLOC_SCRATCH_BYTES inside the library (one per device, kept until
  *   the process ends).  Allocates nothing: no hipMalloc / hipFree, no
  *   allocating library call.  A call whose split would need more scratch
- *   than that returns LTX_EINVAL with a message (at most 512 resident
- *   workgroups x 128 rows x (8 + 2 D) bytes are ever planned on MI355X:
- *   17.3 MB for D = 128).  Calls that overlap in time on one device share the
+ *   than that returns LTX_EINVAL with a message (at most two partial
+ *   results per CU, 512 x 128 rows x (8 + 2 D) bytes, are ever planned on
+ *   MI355X: 17.3 MB for D = 128).  Calls that overlap in time on one device share the
  *   array and race: serialise them (one stream, or events).
  */
 #define LTX_NOALLOC_SCRATCH_BYTES (24ll << 20)

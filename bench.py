@@ -120,10 +120,12 @@ def build_workload(dev, kv_dtype: str = "bf16"):
                 out=torch.empty(B, LQ, H, D, device=dev, dtype=torch.bfloat16))
 
 
-def make_step(w):
+def make_step(w, attn_queries: int = LQ):
     """Returns (step, attn_only, norm_only, append_only, prep) closures over the
     workload; prep is the step's first part: the fused q/k norm + RoPE + V
-    append launch (bf16 arena) or norm then the fp8 pair append."""
+    append launch (bf16 arena) or norm then the fp8 pair append.  attn_queries:
+    the attention call takes the chunk's first attn_queries queries (all by
+    default)."""
     from taomate_amd import kernels
     from taomate_amd.kernels import KVSegment
 
@@ -149,8 +151,10 @@ def make_step(w):
         else:
             kernels.kv_append(w["v_lin"].view(B, LQ, H, D), vd)
 
+    qa, oa = q4[:, :attn_queries], w["out"][:, :attn_queries]
+
     def attn():
-        kernels.flash_attn(q4, segs, w["out"], frame_tokens=frame)
+        kernels.flash_attn(qa, segs, oa, frame_tokens=frame)
 
     def prep():
         if a.fp8:
@@ -435,6 +439,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--attn-only", action="store_true", help="loop only the attention kernel (profiling)")
+    ap.add_argument("--attn-queries", type=int, default=LQ,
+                    help="--attn-only: attend the chunk's first N queries (1024: 8 q-tiles per head, the pair kernel)")
     ap.add_argument("--no-stream", action="store_true", help="skip the 60-chunk long-stream measurement")
     ap.add_argument("--stream-only", action="store_true", help="run only the 60-chunk long-stream measurement")
     ap.add_argument("--no-dit", action="store_true", help="skip the 48-block denoising-step measurement")
@@ -481,12 +487,23 @@ def main():
             del x, y
         return
     w = build_workload(dev, args.kv)
-    step, attn, norm, append, prep = make_step(w)
+    if not 1 <= args.attn_queries <= LQ:
+        print(f"bench.py: --attn-queries must be in [1, {LQ}]", file=sys.stderr)
+        sys.exit(2)
+    step, attn, norm, append, prep = make_step(w, args.attn_queries if args.attn_only else LQ)
     if args.attn_only:
+        prep()  # the chunk's normalised q and new K/V: the attention inputs of a step
+        torch.cuda.synchronize()
+        t_settle = time.perf_counter()
+        while time.perf_counter() - t_settle < args.settle_seconds:
+            for _ in range(20):
+                attn()
+            torch.cuda.synchronize()
         for _ in range(args.warmup):
             attn()
         ms = time_region(attn, args.steps)
-        print(json.dumps({"attn_only_ms": ms, "tflops": attn_flops() / ms / 1e9}))
+        flops = attn_flops() * args.attn_queries / LQ
+        print(json.dumps({"attn_only_ms": ms, "queries": args.attn_queries, "tflops": flops / ms / 1e9}))
         return
     # Settle phase (reported as its own field, outside warmup and steps): the
     # step runs back to back for --settle-seconds of wall time so that the

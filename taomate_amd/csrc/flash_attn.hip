@@ -1379,8 +1379,9 @@ extern "C" int ltx_flash_attn_workspace_size(int64_t B, int64_t Lq, int64_t H, i
     const int64_t nu = kp ? nq / 2 : nq;
     int64_t n_full;
     int split;
+    // with an unbounded key count the planned split is the largest any call of this shape plans
     plan_split(nu, 1 << 30, flash_slots(D, k == 1, k == 2, k == 3, pair), &n_full, &split);
-    const int64_t b = split > 1 ? workspace_bytes_for((nu - n_full) * (kp ? 2 : 1), kMaxSplit, D) : 0;
+    const int64_t b = split > 1 ? workspace_bytes_for((nu - n_full) * (kp ? 2 : 1), split, D) : 0;
     need = b > need ? b : need;
   }
   *bytes = need;

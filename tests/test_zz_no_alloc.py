@@ -35,6 +35,8 @@ def _arena_segments(dev, B, H, D, lens, g):
 @pytest.mark.parametrize("first,second", [
     # (B, Lq, H, D, segment lengths): 576 then 520 q-tiles of 128 on 512 resident slots
     ((2, 1152, 32, 128, [384, 768, 2304, 1152]), (1, 1664, 40, 128, [512, 1536])),
+    # even q-tile counts per head (the pair kernel): 320 then 280 units of two q-tiles on 256
+    ((2, 1280, 32, 128, [1024, 1024]), (1, 1792, 40, 128, [512, 1536])),
 ])
 def test_noalloc_matches_workspace_entry_point(dev, first, second):
     g = gen(21)

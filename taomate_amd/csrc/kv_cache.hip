@@ -30,7 +30,7 @@ __global__ void kv_copy_kernel(const TS* __restrict__ src, int64_t s_bs, int64_t
   const TS* s = src + b * s_bs + l * s_ls + h * s_hs + c * 8;
   uint16_t* d = dst + b * d_bs + l * d_ls + h * d_hs + c * 8;
   if constexpr (sizeof(TS) == 2) {
-    *reinterpret_cast<uint4*>(d) = *reinterpret_cast<const uint4*>(s);
+    store_stream(d, *reinterpret_cast<const uint4*>(s));
   } else {
     float4 a = reinterpret_cast<const float4*>(s)[0];
     float4 bb = reinterpret_cast<const float4*>(s)[1];
@@ -39,7 +39,7 @@ __global__ void kv_copy_kernel(const TS* __restrict__ src, int64_t s_bs, int64_t
     o.y = pack_bf16x2(a.z, a.w);
     o.z = pack_bf16x2(bb.x, bb.y);
     o.w = pack_bf16x2(bb.z, bb.w);
-    *reinterpret_cast<uint4*>(d) = o;
+    store_stream(d, o);
   }
 }
 
@@ -91,7 +91,7 @@ __global__ void __launch_bounds__(kQuantThreads) kv_quant_kernel(
     const uint32_t lo = pack4_e4m3(q[0], q[1], q[2], q[3]);
     const uint32_t hi = pack4_e4m3(q[4], q[5], q[6], q[7]);
     const int t = idx / cpr, c = idx % cpr;
-    *reinterpret_cast<uint2*>(dbase + (int64_t)t * d_ls + c * 8) = make_uint2(lo, hi);
+    store_stream(dbase + (int64_t)t * d_ls + c * 8, make_uint2(lo, hi));
   };
 
   float v[kQuantRegs][8];
@@ -212,8 +212,8 @@ __global__ void __launch_bounds__(kPairThreads) kv_quant_pair_kernel(const Quant
     }
     quotients_e4m3_bf16(x, sc, rc, corrected, q);
     const int t = idx / cpr, c = idx % cpr;
-    *reinterpret_cast<uint2*>(dbase + ((Off)t * d_ls + c * 8)) =
-        make_uint2(pack4_e4m3(q[0], q[1], q[2], q[3]), pack4_e4m3(q[4], q[5], q[6], q[7]));
+    store_stream(dbase + ((Off)t * d_ls + c * 8),
+                 make_uint2(pack4_e4m3(q[0], q[1], q[2], q[3]), pack4_e4m3(q[4], q[5], q[6], q[7])));
   };
 
   uint4 raw[kPairRegs];

@@ -61,7 +61,7 @@ __device__ __forceinline__ void kv_transpose_tile(const TS* __restrict__ src, in
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         w[i] = (uint32_t)tile[(t0 + 2 * i) * RS + d] | ((uint32_t)tile[(t0 + 2 * i + 1) * RS + d] << 16);
-      *reinterpret_cast<uint4*>(dp) = make_uint4(w[0], w[1], w[2], w[3]);
+      store_stream(dp, make_uint4(w[0], w[1], w[2], w[3]));
     } else {
       for (int i = 0; t0 + i < rows; ++i) dp[i] = tile[(t0 + i) * RS + d];
     }

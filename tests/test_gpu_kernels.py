@@ -347,6 +347,10 @@ ATTN_CASES = [
     # the 16-segment maximum (after the two empty ones are dropped), ragged
     (1, 64, 4, 128, [8, 0, 17, 64, 1, 130, 9, 33, 0, 64, 2, 71, 5, 40, 16, 3, 7, 11]),
     (1, 128, 8, 128, [40000, 128]),               # long key range: 627 key tiles
+    # two q-tiles per head (key-major V: the two-q-tile workgroup kernel), the
+    # second one ragged, at the segment maximum and over a long key range
+    (1, 200, 4, 128, [8, 0, 17, 64, 1, 130, 9, 33, 0, 64, 2, 71, 5, 40, 16, 3, 7, 11]),
+    (1, 250, 8, 128, [40000, 128]),
 ]
 
 

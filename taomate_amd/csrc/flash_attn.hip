@@ -47,6 +47,7 @@ struct FlashParams {
   const float* mask;
   int64_t q_bs, q_ls, q_hs;
   int64_t o_bs, o_ls, o_hs;
+  int o_al16;                        // o and its strides are 16-byte aligned (staged output stores)
   int64_t kv_bs, kv_ls, kv_hs;      // K (and token-major V) strides
   int64_t v_bs, v_hs, v_ds;          // key-major V: element (b, t, h, d) at b*v_bs + h*v_hs + d*v_ds + t
   int64_t sc_bs, sc_hs;
@@ -239,13 +240,60 @@ __device__ __forceinline__ WorkItem pair_work(const FlashParams& p, int bid, int
 // Epilogue shared by the kernels: normalise and store a whole q-tile, or
 // store a key range's partial result (unnormalised O, running max and sum).  oacc holds O^T fragments (lane: query li,
 // d = db*32 + 8*(r/4) + 4*hg + r%4); m_run / l_tot are per query.
+//
+// stage (the pipelined kernels): this wave's 32 x (D + 8) bf16 region of LDS,
+// free once every wave is past its last K/V tile.  The wave's 32 rows go
+// through it so that each store writes 16 bytes per lane and a store
+// instruction covers whole rows (four 256-byte rows at D = 128) instead of 16
+// bytes of each of 32 rows 8 KB apart: an eighth of the memory requests.
+// Every wave of the workgroup calls it (two barriers inside), with one path
+// for the whole workgroup (a whole q-tile or a key range, and o_al16).
 template <int D>
 __device__ __forceinline__ void finish_tile(const FlashParams& p, const WorkItem& w, int b, int h,
                                             int qt, int row, const f32x16_t (&oacc)[D / 32], float m_run,
-                                            float l_tot) {
+                                            float l_tot, uint16_t* stage = nullptr) {
   constexpr int DB = D / 32;
   const int hg = (threadIdx.x & 63) >> 5;  // row: this lane's query inside the q-tile
   const int qi = qt * kBM + row;
+  if (stage != nullptr && (w.piece >= 0 || p.o_al16)) {
+    constexpr int RS = D + 8;   // staging row stride (elements)
+    constexpr int CPR = D / 8;  // 16-byte chunks per row
+    const int li = threadIdx.x & 31, lane = threadIdx.x & 63;
+    const int row0 = row - li;  // the wave's first row in the q-tile
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    __syncthreads();  // every wave is done reading the K/V tiles
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        uint2 v;
+        v.x = pack_bf16x2(oacc[d][4 * g4] * inv, oacc[d][4 * g4 + 1] * inv);
+        v.y = pack_bf16x2(oacc[d][4 * g4 + 2] * inv, oacc[d][4 * g4 + 3] * inv);
+        *reinterpret_cast<uint2*>(stage + li * RS + d * 32 + 8 * g4 + 4 * hg) = v;
+      }
+    __syncthreads();
+    if (w.piece < 0) {
+      const int64_t obase = b * p.o_bs + h * p.o_hs;
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) {
+        const int c = i * 64 + lane, r = c / CPR, cc = c % CPR;
+        const int q = qt * kBM + row0 + r;
+        const uint4 v = *reinterpret_cast<const uint4*>(stage + r * RS + cc * 8);
+        if (q < p.Lq) *reinterpret_cast<uint4*>(p.o + obase + (int64_t)q * p.o_ls + cc * 8) = v;
+      }
+      if (p.lse != nullptr && hg == 0 && qi < p.Lq)
+        p.lse[((int64_t)b * p.H + h) * p.Lq + qi] = (m_run + __log2f(l_tot)) / kLog2e;
+    } else {
+      uint16_t* po = p.part_o + ((int64_t)w.piece * kBM + row0) * D;
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) {
+        const int c = i * 64 + lane, r = c / CPR, cc = c % CPR;
+        *reinterpret_cast<uint4*>(po + r * D + cc * 8) = *reinterpret_cast<const uint4*>(stage + r * RS + cc * 8);
+      }
+      if (hg == 0) *reinterpret_cast<float2*>(p.part_ml + ((int64_t)w.piece * kBM + row) * 2) = make_float2(m_run, l_tot);
+    }
+    return;
+  }
   if (w.piece < 0) {
     if (qi < p.Lq) {
       const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
@@ -1210,8 +1258,11 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
       pv_tile(0, pa);
   }
 
-  finish_tile<D>(p, wi, b, h, qt, (PAIR ? wave : (int)(threadIdx.x >> 6)) * 32 + (int)(threadIdx.x & 31), oacc,
-                 m_run, pair_sum(l_run));
+  // output staging: waves 0-3 in the K buffers, the pair kernel's group 1 in the V buffers
+  static_assert(4 * 32 * (D + 8) <= 2 * KBUF && 4 * 32 * (D + 8) <= 2 * VBUF, "output staging region");
+  const int owave = PAIR ? wave : (int)(threadIdx.x >> 6);
+  uint16_t* stage = (PAIR && grp == 1 ? &vbuf[0][0] : &kbuf[0][0]) + owave * 32 * (D + 8);
+  finish_tile<D>(p, wi, b, h, qt, owave * 32 + (int)(threadIdx.x & 31), oacc, m_run, pair_sum(l_run), stage);
 }
 
 template <int D, bool FP8>
@@ -1438,6 +1489,7 @@ static int flash_attn_fwd_impl(const void* q, int64_t B, int64_t Lq, int64_t H, 
   p.mask = key_mask;
   p.q_bs = q_bs; p.q_ls = q_ls; p.q_hs = q_hs;
   p.o_bs = o_bs; p.o_ls = o_ls; p.o_hs = o_hs;
+  p.o_al16 = ((uintptr_t)out % 16 == 0 && o_bs % 8 == 0 && o_ls % 8 == 0 && o_hs % 8 == 0) ? 1 : 0;
   p.kv_bs = k_bs; p.kv_ls = k_ls; p.kv_hs = k_hs;
   p.v_bs = v_bs; p.v_hs = v_hs; p.v_ds = v_ds;
   p.sc_bs = sc_bs; p.sc_hs = sc_hs;

@@ -246,8 +246,12 @@ __device__ __forceinline__ WorkItem pair_work(const FlashParams& p, int bid, int
 // through it so that each store writes 16 bytes per lane and a store
 // instruction covers whole rows (four 256-byte rows at D = 128) instead of 16
 // bytes of each of 32 rows 8 KB apart: an eighth of the memory requests.
-// Every wave of the workgroup calls it (two barriers inside), with one path
-// for the whole workgroup (a whole q-tile or a key range, and o_al16).
+// The stores are streaming ones (whole rows now, so they leave the L2 as
+// full lines while the kernel runs): 156.3 -> 154.0 us for the staging and
+// 152.6 us with streaming stores at the 1152 x 4608 chunk, and the launch
+// after it 1.5 us faster.  Every wave of the workgroup calls it (two
+// barriers inside), with one path for the whole workgroup (a whole q-tile or
+// a key range, and o_al16).
 template <int D>
 __device__ __forceinline__ void finish_tile(const FlashParams& p, const WorkItem& w, int b, int h,
                                             int qt, int row, const f32x16_t (&oacc)[D / 32], float m_run,
@@ -279,7 +283,7 @@ __device__ __forceinline__ void finish_tile(const FlashParams& p, const WorkItem
         const int c = i * 64 + lane, r = c / CPR, cc = c % CPR;
         const int q = qt * kBM + row0 + r;
         const uint4 v = *reinterpret_cast<const uint4*>(stage + r * RS + cc * 8);
-        if (q < p.Lq) *reinterpret_cast<uint4*>(p.o + obase + (int64_t)q * p.o_ls + cc * 8) = v;
+        if (q < p.Lq) store_stream(p.o + obase + (int64_t)q * p.o_ls + cc * 8, v);
       }
       if (p.lse != nullptr && hg == 0 && qi < p.Lq)
         p.lse[((int64_t)b * p.H + h) * p.Lq + qi] = (m_run + __log2f(l_tot)) / kLog2e;
@@ -288,7 +292,7 @@ __device__ __forceinline__ void finish_tile(const FlashParams& p, const WorkItem
 #pragma unroll
       for (int i = 0; i < D / 16; ++i) {
         const int c = i * 64 + lane, r = c / CPR, cc = c % CPR;
-        *reinterpret_cast<uint4*>(po + r * D + cc * 8) = *reinterpret_cast<const uint4*>(stage + r * RS + cc * 8);
+        store_stream(po + r * D + cc * 8, *reinterpret_cast<const uint4*>(stage + r * RS + cc * 8));
       }
       if (hg == 0) *reinterpret_cast<float2*>(p.part_ml + ((int64_t)w.piece * kBM + row) * 2) = make_float2(m_run, l_tot);
     }

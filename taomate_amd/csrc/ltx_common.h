@@ -55,9 +55,11 @@ typedef float ltx_f32x2_t __attribute__((ext_vector_type(2)));
 // L2 and are written back when the kernel ends, a phase with no other work;
 // streaming stores leave the L2 while the kernel still runs.  Measured at a
 // 1152-token chunk of 32 x 128 heads, B = 2: the fp8 K+V quantise 12.9 ->
-// 10.4 us, the key-major V append 6.7 -> 5.5 us.  The attention output's
-// scattered 8-byte stores got slower this way (159 -> 176 us per call), so
-// they stay ordinary; the norm + RoPE rows showed no change.
+// 10.4 us, the key-major V append 6.7 -> 5.5 us.  Stores that cover only
+// part of a line per instruction got slower this way (the attention output
+// written 8 bytes per lane over 32 rows: 159 -> 176 us per call), so the
+// attention stages its output to whole rows first; the norm + RoPE rows
+// showed no change.
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void store_stream(void* p, uint4 v) {

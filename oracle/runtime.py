@@ -130,10 +130,11 @@ class StreamOracle:
                                        learned_memory_color=cond.get("learned_memory_color"), return_caches=True)
         return vo.view(B, F_, H, W, C).permute(0, 1, 4, 2, 3), ao, new
 
-    def _block(self, blk, B, C, cond, first_of_stream: bool):
-        bi, vs, ve, as_, ae = blk
-        c = self._cond(cond)
-        pre = self.layers
+    def _denoise(self, blk, B, C, c, pre):
+        """_denoise_block_with_kv (model_runtime.py:847-962): pure noise, then per
+        step the prefix-only cache (``pre``, restored every step), x0 = x - v*sigma,
+        and re-noise with the NEXT sigma while it is above 0."""
+        _, vs, ve, as_, ae = blk
         H, W = self.hw
         video = self.noise((B, ve - vs, C, H, W))
         audio = self.noise((B, ae - as_, C))
@@ -146,15 +147,36 @@ class StreamOracle:
                 n = sig[si + 1].expand(B)
                 video = add_noise(video, self.noise(tuple(video.shape)), n)
                 audio = add_noise(audio, self.noise(tuple(audio.shape)), n)
+        return video, audio
+
+    def _stabilize(self, bi, video):
+        """_maybe_renorm_block (model_runtime.py:732-770), anchor block 0, video only."""
         if self.renorm:
             if bi == 0:
                 self.anchor = channel_stats(video)
             elif self.anchor is not None:
                 video = apply_renorm(video, self.anchor, self.alpha)
+        return video
+
+    def _commit(self, blk, video, audio, c, pre, first_of_stream: bool):
+        """_commit_clean_block (model.py:88-129): sigma 0 over the block's final
+        latents, appended to the pre-block layers (a fresh cache for block 0)."""
+        B = video.shape[0]
+        _, _, self.layers = self._forward(blk, video, audio, torch.zeros(B), c, None if first_of_stream else pre)
+
+    def _block(self, blk, B, C, cond, first_of_stream: bool):
+        """One block in the reference's order (model.py:200-243;
+        model_runtime.py:1160-1325): conditioning from the memory, denoise,
+        renorm, colour correction, clean commit, then set_reference (block 0)
+        and update."""
+        bi = blk[0]
+        c = self._cond(cond)
+        pre = self.layers
+        video, audio = self._denoise(blk, B, C, c, pre)
+        video = self._stabilize(bi, video)
         if self.memory is not None:
             video = torch.from_numpy(self.memory.apply_color(video.double().numpy())).float()
-        # clean commit: sigma 0 over the block, appended to the pre-block layers
-        _, _, self.layers = self._forward(blk, video, audio, torch.zeros(B), c, None if first_of_stream else pre)
+        self._commit(blk, video, audio, c, pre, first_of_stream)
         if self.memory is not None:
             if first_of_stream:
                 self.memory.set_reference(video.double().numpy(), audio.double().numpy())
@@ -192,19 +214,32 @@ class StreamOracle:
         ``cond`` at their global block positions, from an empty cache.
         Returns the rebuilt layers (the caller keeps their audio self, A2V and
         V2A fields)."""
-        total = prefix_video.shape[1] + next_frames
-        prefix_blocks = [b for b in compute_blocks(total) if b[2] <= prefix_video.shape[1]]
-        has_sink = segments[0]["block_idx"] == 0
-        warm = len(segments) - int(has_sink)
-        cands = prefix_blocks[1:] if has_sink else prefix_blocks
-        selected = ([prefix_blocks[0]] if has_sink else []) + (cands[-warm:] if warm else [])
-        assert len(selected) == len(segments)
         layers = None
-        for lb, seg in zip(selected, segments):
-            k = int(seg["block_idx"])
-            gb = compute_blocks(4 + k * 3)[k]
+        for lb, gb in refresh_selection(segments, prefix_video.shape[1], next_frames):
             video = prefix_video[:, lb[1]:lb[2]]
             audio = prefix_audio[:, lb[3]:lb[4]]
             B = video.shape[0]
             _, _, layers = self._forward(gb, video, audio, torch.zeros(B), self._cond(cond), layers)
         return layers
+
+
+def global_block(k: int):
+    """_global_block (taomate/inference/runtime.py:365-371): block k of a stream
+    of 4 + 3k frames."""
+    return compute_blocks(4 + int(k) * 3)[int(k)]
+
+
+def refresh_selection(segments, prefix_frames: int, next_frames: int):
+    """The (local prefix block, global block) pairs _refresh_conditioning_cache
+    re-runs (taomate/inference/runtime.py:400-414, 427): the prefix's blocks
+    among those of prefix + next frames; the sink block first when the cache
+    holds block 0, then the last ``warm`` prefix blocks; each paired with the
+    global block of its segment's block index."""
+    prefix_blocks = [b for b in compute_blocks(int(prefix_frames) + int(next_frames)) if b[2] <= prefix_frames]
+    has_sink = int(segments[0]["block_idx"]) == 0
+    warm = len(segments) - int(has_sink)
+    cands = prefix_blocks[1:] if has_sink else prefix_blocks
+    selected = ([prefix_blocks[0]] if has_sink else []) + (cands[-warm:] if warm else [])
+    if len(selected) != len(segments):
+        raise RuntimeError("The retained latent prefix does not match the cache layout.")
+    return [(lb, global_block(seg["block_idx"])) for lb, seg in zip(selected, segments)]

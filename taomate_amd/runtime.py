@@ -126,6 +126,26 @@ def video_latent(tokens: torch.Tensor, frames: int, hw: Tuple[int, int]) -> torc
 NoiseFn = Callable[[Tuple[int, ...], torch.device, torch.dtype], torch.Tensor]
 
 
+def refresh_selection(segments: Sequence[Dict[str, Any]], prefix_frames: int,
+                      next_frames: int) -> List[Tuple[AVBlock, AVBlock]]:
+    """The (prefix block, global block) pairs a prompt-change refresh re-runs
+    (taomate/inference/runtime.py:400-414, 427): the prefix's blocks among the
+    4-3-3 blocks of prefix + next frames; the sink block first when the cache
+    holds block 0, then the last ``len(segments) - sink`` prefix blocks, each
+    paired with the global block of its segment's index.  A prefix holding
+    fewer blocks than the cache's segments is an error."""
+    local = compute_av_blocks(int(prefix_frames) + int(next_frames), FRAMES_PER_BLOCK, FIRST_BLOCK_FRAMES)
+    prefix_blocks = [b for b in local if b.video_end <= prefix_frames]
+    has_sink = int(segments[0]["block_idx"]) == 0
+    warm = len(segments) - int(has_sink)
+    candidates = prefix_blocks[1:] if has_sink else prefix_blocks
+    selected = ([prefix_blocks[0]] if has_sink else []) + (candidates[-warm:] if warm else [])
+    if len(selected) != len(segments):
+        raise RuntimeError("The retained latent prefix does not match the cache layout.")
+    return [(lb, global_block_at_index(int(seg["block_idx"]), FRAMES_PER_BLOCK, FIRST_BLOCK_FRAMES))
+            for lb, seg in zip(selected, segments)]
+
+
 class StreamingGenerator:
     """Block loop of one stream on an ``AVModel`` (taomate/inference/model.py:33-248).
 
@@ -413,20 +433,11 @@ class StreamingGenerator:
                 int(prefix_video.shape[1]), FRAMES_PER_BLOCK, FIRST_BLOCK_FRAMES):
             raise RuntimeError(f"Prefix alignment mismatch: {prefix_video.shape[1]} video frames, "
                                f"{None if prefix_audio is None else prefix_audio.shape[1]} audio frames.")
-        total = int(prefix_video.shape[1]) + int(next_video_shape[1])
-        local = compute_av_blocks(total, FRAMES_PER_BLOCK, FIRST_BLOCK_FRAMES)
-        prefix_blocks = [b for b in local if b.video_end <= prefix_video.shape[1]]
-        has_sink = int(segments[0]["block_idx"]) == 0
-        warm = len(segments) - int(has_sink)
-        candidates = prefix_blocks[1:] if has_sink else prefix_blocks
-        selected = ([prefix_blocks[0]] if has_sink else []) + (candidates[-warm:] if warm else [])
-        if len(selected) != len(segments):
-            raise RuntimeError("The retained latent prefix does not match the cache layout.")
+        pairs = refresh_selection(segments, int(prefix_video.shape[1]), int(next_video_shape[1]))
         dev = cond["video_context"].device
         dtype = self.model.patchify_proj.weight.dtype
         rebuilt = self.init_kv_cache()
-        for lb, seg in zip(selected, segments):
-            gb = global_block_at_index(int(seg["block_idx"]), FRAMES_PER_BLOCK, FIRST_BLOCK_FRAMES)
+        for lb, gb in pairs:
             video = prefix_video[:, lb.video_start:lb.video_end].to(device=dev, dtype=dtype)
             audio = prefix_audio[:, lb.audio_start:lb.audio_end].to(device=dev, dtype=dtype)
             bc = self._with_memory(memory, cond, dev, dtype)

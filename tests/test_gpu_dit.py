@@ -238,3 +238,38 @@ def test_per_frame_sigma_matches_oracle(dev):
     for out, ref in ((vo, ref_v), (ao, ref_a)):
         err = (out.float().cpu() - ref).abs().max().item()
         assert err <= 3e-2 * ref.abs().max().item(), err
+
+
+def test_loaded_checkpoint_matches_oracle(dev, tmp_path):
+    """Weights that came through the disk format: a generator saved in the
+    load_model_generator layout (taomate/inference/model_runtime.py:182-425),
+    loaded with load_generator onto the GPU (configuration detected from the
+    tensors), runs forward_chunk; the oracle runs on the tensors read back
+    from the same file."""
+    from taomate_amd import checkpoint as C
+    src = D.build_model(CFG, dev, seed=11)
+    path = str(tmp_path / "gen.pt")
+    C.save_generator(src, path)
+    del src
+    model = C.load_generator(path, device=dev, dtype=torch.bfloat16, video_d_head=CFG.video_d_head,
+                             audio_d_head=CFG.audio_d_head)
+    assert model.cfg.num_layers == CFG.num_layers and model.cfg.video_heads == CFG.video_heads
+    params = {n: p.float() for n, p in C.read_generator_state(path).items()}
+    x = _inputs()
+    ref_v, ref_a = OD.forward_chunk(params, CFG, x["video"], x["audio"], x["sigma"], x["vctx"], x["actx"],
+                                    x["mask"].float(), x["mask"].float(), *_pes(), x["cache"])
+    hw = GH * GW
+    bf = lambda t: t.to(dev, torch.bfloat16)
+    caches = [T.LayerKVCache(video_self_k=bf(c["video_self_k"]), video_self_v=bf(c["video_self_v"]),
+                             audio_self_k=bf(c["audio_self_k"]), audio_self_v=bf(c["audio_self_v"]))
+              for c in x["cache"]]
+    with torch.no_grad():
+        vo, ao, _ = model.forward_chunk(bf(x["video"]), bf(x["audio"]), x["sigma"].to(dev), bf(x["vctx"]),
+                                        bf(x["actx"]), bf(x["mask"]), bf(x["mask"]), *_pes(dev), caches)
+    torch.cuda.synchronize()
+    assert vo.shape == (B, NF * hw, CFG.out_channels)
+    cv, ca = cosine(vo, ref_v), cosine(ao, ref_a)
+    assert cv >= 0.999 and ca >= 0.999, (cv, ca)
+    for out, ref in ((vo, ref_v), (ao, ref_a)):
+        err = (out.float().cpu() - ref).abs().max().item()
+        assert err <= 3e-2 * ref.abs().max().item(), err

@@ -428,6 +428,118 @@ def cpu_baseline(seconds_budget: float = 20.0):
                       f"torch {torch.__version__}, {platform.processor() or platform.machine()}"}
 
 
+def measure_steps(step, attn, norm, append, prep, steps: int, warmup: int, settle_seconds: float) -> dict:
+    """The C2 step timings for one workload: settle, warm-up, the K timed steps
+    (events only at the two ends of the region), an instrumented pass of K
+    steps with events around each step's two parts, and the two HBM kernels
+    and the step's first part on their own."""
+    # Settle phase (reported as its own field, outside warmup and steps): the
+    # step runs back to back for --settle-seconds of wall time so that the
+    # card leaves its idle clock state before the warm-up and timed steps; a
+    # cold card runs its first milliseconds of work at a lower clock.
+    settle_steps = 0
+    torch.cuda.synchronize()
+    t_settle = time.perf_counter()
+    while time.perf_counter() - t_settle < settle_seconds:
+        for _ in range(20):
+            step()
+        settle_steps += 20
+        torch.cuda.synchronize()
+    settle_s = time.perf_counter() - t_settle
+    for _ in range(warmup):
+        step()
+    # Timed region: the K steps the driver asks for, bracketed by
+    # synchronisations, with HIP events only at its two ends.  (On this
+    # runtime an event recorded between two kernels holds the second one back
+    # by about 5 us, so per-call events inside this loop would add about
+    # 15 us to every step.)
+    st = torch.cuda.current_stream()
+    e_start, e_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e_start.record(st)
+    for i in range(steps):
+        step()
+    t_enq = time.perf_counter() - t0   # host time to queue the K steps
+    e_end.record(st)
+    e_end.synchronize()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = e_start.elapsed_time(e_end) / steps
+    # Instrumented pass: K more steps with events on the launching stream
+    # around each step's two parts (q/k norm + RoPE + V append, attention),
+    # for the per-step distributions and the in-step split.
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        e = ev[i]
+        e[0].record(st)
+        prep()
+        e[1].record(st)
+        attn()
+        e[2].record(st)
+    torch.cuda.synchronize()
+    prep_ms = [e[0].elapsed_time(e[1]) for e in ev]
+    attn_ms = [e[1].elapsed_time(e[2]) for e in ev]
+    step_ms = [e[0].elapsed_time(e[2]) for e in ev]
+    ms_prep = sum(prep_ms) / steps
+    # The attention call's average duration inside the step (the roofline's
+    # kernel_ms): events around each call in the instrumented pass.  The same
+    # calls back to back, with no other kernel between them, measured 1-2 %
+    # slower (170-173 against 169-170 us at the 512x768 chunk), so that figure
+    # is reported beside it.
+    ms_attn = sum(attn_ms) / steps
+    ms_attn_b2b = time_region(attn, steps)
+    # the two HBM kernels on their own (after the timed region), for their rates
+    for _ in range(10):
+        norm()
+        append()
+    ms_norm = time_region(norm, 50)
+    ms_app = time_region(append, 50)
+    # the step's first part on its own: as launched in the step, and as the
+    # two separate launches (norm, then append) it replaces
+    ms_prep_alone = time_region(prep, 50)
+    ms_prep_two = time_region(lambda: (norm(), append()), 50)
+    return dict(ms_step=ms_step, ms_attn=ms_attn, ms_attn_b2b=ms_attn_b2b, ms_prep=ms_prep, ms_norm=ms_norm,
+                ms_app=ms_app, ms_prep_alone=ms_prep_alone, ms_prep_two=ms_prep_two, step_ms=step_ms,
+                attn_ms=attn_ms, prep_ms=prep_ms, settle_s=settle_s, settle_steps=settle_steps, wall=wall,
+                t_enq=t_enq)
+
+
+def fp8_step_bench(dev, steps: int, warmup: int, settle_seconds: float) -> dict:
+    """The same C2 step on an fp8-e4m3 arena (per-(batch, head, frame) scales),
+    measured in the same run and the same way as the headline line: q/k norm +
+    RoPE (K to a bf16 buffer), the K and V quantise into the arena (one
+    launch), then attention over the dequantised-in-kernel cache."""
+    w = build_workload(dev, "fp8")
+    step, attn, norm, append, prep = make_step(w)
+    m = measure_steps(step, attn, norm, append, prep, steps, warmup, settle_seconds)
+    del step, attn, norm, append, prep, w
+    fl = attn_flops()
+    ach = fl / (m["ms_attn"] * 1e-3) / 1e12
+    prep_bytes = norm_rope_bytes() + append_bytes("fp8")
+    return {
+        "query_tokens_per_s": B * LQ / (m["ms_step"] * 1e-3),
+        "ms_per_step": m["ms_step"],
+        "attention": {"kernel": "flash_fwd_pipe_kernel<128, true> + flash_combine_kernel<128>",
+                      "kernel_ms": m["ms_attn"], "kernel_ms_back_to_back": m["ms_attn_b2b"],
+                      "tflops": ach, "frac_bf16_peak": ach / PEAK_BF16_TFLOPS,
+                      "algorithmic_bytes": attn_bytes(1), "traffic": measured_traffic("fp8")},
+        "quantise": {"ms": m["ms_app"], "GB/s": append_bytes("fp8") / (m["ms_app"] * 1e-3) / 1e9,
+                     "frac_hbm": append_bytes("fp8") / (m["ms_app"] * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+                     "what": "K and V quantised to e4m3 into the arena (one launch, run on its own)"},
+        "norm_rope": {"ms": m["ms_norm"], "GB/s": norm_rope_bytes() / (m["ms_norm"] * 1e-3) / 1e9,
+                      "frac_hbm": norm_rope_bytes() / (m["ms_norm"] * 1e-3) / 1e9 / PEAK_HBM_GBPS},
+        "step_prep": {"ms": m["ms_prep"], "alone_ms": m["ms_prep_alone"],
+                      "GB/s": prep_bytes / (m["ms_prep"] * 1e-3) / 1e9,
+                      "frac_hbm": prep_bytes / (m["ms_prep"] * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+                      "what": "q/k norm + RoPE, then the fp8 pair append (in the step)"},
+        "per_step_ms_median": {"step": statistics.median(m["step_ms"]),
+                               "attention": statistics.median(m["attn_ms"]),
+                               "prep": statistics.median(m["prep_ms"])},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -441,6 +553,7 @@ def main():
     ap.add_argument("--attn-only", action="store_true", help="loop only the attention kernel (profiling)")
     ap.add_argument("--attn-queries", type=int, default=LQ,
                     help="--attn-only: attend the chunk's first N queries (1024: 8 q-tiles per head, the pair kernel)")
+    ap.add_argument("--no-fp8", action="store_true", help="skip the same step on the fp8-e4m3 arena (its own object)")
     ap.add_argument("--no-stream", action="store_true", help="skip the 60-chunk long-stream measurement")
     ap.add_argument("--stream-only", action="store_true", help="run only the 60-chunk long-stream measurement")
     ap.add_argument("--no-dit", action="store_true", help="skip the 48-block denoising-step measurement")
@@ -505,76 +618,15 @@ def main():
         flops = attn_flops() * args.attn_queries / LQ
         print(json.dumps({"attn_only_ms": ms, "queries": args.attn_queries, "tflops": flops / ms / 1e9}))
         return
-    # Settle phase (reported as its own field, outside warmup and steps): the
-    # step runs back to back for --settle-seconds of wall time so that the
-    # card leaves its idle clock state before the warm-up and timed steps; a
-    # cold card runs its first milliseconds of work at a lower clock.
-    settle_steps = 0
-    torch.cuda.synchronize()
-    t_settle = time.perf_counter()
-    while time.perf_counter() - t_settle < args.settle_seconds:
-        for _ in range(20):
-            step()
-        settle_steps += 20
-        torch.cuda.synchronize()
-    settle_s = time.perf_counter() - t_settle
-    for _ in range(args.warmup):
-        step()
-    # Timed region: the K steps the driver asks for, bracketed by
-    # synchronisations, with HIP events only at its two ends.  (On this
-    # runtime an event recorded between two kernels holds the second one back
-    # by about 5 us, so per-call events inside this loop would add about
-    # 15 us to every step.)
-    st = torch.cuda.current_stream()
-    e_start, e_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e_start.record(st)
-    for i in range(args.steps):
-        step()
-    t_enq = time.perf_counter() - t0   # host time to queue the K steps
-    e_end.record(st)
-    e_end.synchronize()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = e_start.elapsed_time(e_end) / args.steps
-    # Instrumented pass: K more steps with events on the launching stream
-    # around each step's two parts (q/k norm + RoPE + V append, attention),
-    # for the per-step distributions and the in-step split.
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    for i in range(args.steps):
-        e = ev[i]
-        e[0].record(st)
-        prep()
-        e[1].record(st)
-        attn()
-        e[2].record(st)
-    torch.cuda.synchronize()
-    prep_ms = [e[0].elapsed_time(e[1]) for e in ev]
-    attn_ms = [e[1].elapsed_time(e[2]) for e in ev]
-    step_ms = [e[0].elapsed_time(e[2]) for e in ev]
-    ms_prep = sum(prep_ms) / args.steps
-    # The attention call's average duration inside the step (the roofline's
-    # kernel_ms): events around each call in the instrumented pass.  The same
-    # calls back to back, with no other kernel between them, measured 1-2 %
-    # slower (170-173 against 169-170 us at the 512x768 chunk), so that figure
-    # is reported beside it.
-    ms_attn = sum(attn_ms) / args.steps
-    ms_attn_b2b = time_region(attn, args.steps)
+    m = measure_steps(step, attn, norm, append, prep, args.steps, args.warmup, args.settle_seconds)
+    del step, attn, norm, append, prep, w
+    ms_step, ms_attn, ms_attn_b2b, ms_prep = m["ms_step"], m["ms_attn"], m["ms_attn_b2b"], m["ms_prep"]
+    ms_norm, ms_app, ms_prep_alone, ms_prep_two = m["ms_norm"], m["ms_app"], m["ms_prep_alone"], m["ms_prep_two"]
+    step_ms, attn_ms, prep_ms = m["step_ms"], m["attn_ms"], m["prep_ms"]
+    settle_s, settle_steps, wall, t_enq = m["settle_s"], m["settle_steps"], m["wall"], m["t_enq"]
 
     def dist(xs):
         return {"min": min(xs), "median": statistics.median(xs), "max": max(xs)}
-    # the two HBM kernels on their own (after the timed region), for their rates
-    for _ in range(10):
-        norm()
-        append()
-    ms_norm = time_region(norm, 50)
-    ms_app = time_region(append, 50)
-    # the step's first part on its own: as launched in the step, and as the
-    # two separate launches (norm, then append) it replaces
-    ms_prep_alone = time_region(prep, 50)
-    ms_prep_two = time_region(lambda: (norm(), append()), 50)
     kvb = 1 if args.kv == "fp8" else 2
     fl = attn_flops()
     ach = fl / (ms_attn * 1e-3) / 1e12
@@ -629,6 +681,8 @@ def main():
         "wall_s_timed_region": wall,
         "host_enqueue_ms_per_step": t_enq * 1e3 / args.steps,
     }
+    if args.kv == "bf16" and not args.no_fp8:
+        res["fp8"] = fp8_step_bench(dev, args.steps, args.warmup, args.settle_seconds)
     if not args.no_stream:
         res["long_stream"] = stream_bench(dev, fuse_qkv=not args.no_fuse_qkv)
     if not args.no_dit:

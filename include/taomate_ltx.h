@@ -27,8 +27,9 @@
 extern "C" {
 #endif
 
-#define LTX_ABI_VERSION 1
+#define LTX_ABI_VERSION 2
 #define LTX_MAX_SEGMENTS 16
+#define LTX_MAX_KEYLEN_BATCH 16   /* batch rows ltx_flash_attn_fwd's key_lens covers */
 
 typedef enum {
   LTX_F32 = 0,
@@ -205,6 +206,12 @@ int ltx_kv_gather(int64_t elem_bytes, int64_t B, int64_t H, int64_t D, const voi
  *   key_mask: NULL or float32 additive mask [B, Lk_total] with batch stride
  *   mask_bs (the reference's `(m - 1) * finfo.max` padding mask,
  *   ltx_causal/transformer/causal_model.py:551-562); token-major V only.
+ *   key_lens: NULL, or a host array of B key counts (B <= LTX_MAX_KEYLEN_BATCH):
+ *   batch row b attends keys [0, key_lens[b]) of the concatenated sequence
+ *   only, each count in [0, Lk_total].  This is that padding mask when every
+ *   row keeps a prefix of its keys (the masked keys' weights are exactly 0 in
+ *   float32), run on the pipelined kernel; bf16 key-major V, no key_mask.  A
+ *   row with no keys gets a zero output.
  *   lse: NULL or float32 [B, H, Lq] natural-log sum-exp of the scaled logits.
  *   scale <= 0 selects 1/sqrt(D) (SDPA's default).
  *   workspace: NULL, or workspace_bytes >= ltx_flash_attn_workspace_size() of
@@ -213,7 +220,7 @@ int ltx_kv_gather(int64_t elem_bytes, int64_t B, int64_t H, int64_t D, const voi
  *   and recombined by a second kernel on `stream`, so the grid ends together;
  *   without it they run whole.  Calls that overlap in time must use different
  *   workspaces.
- *   Host arrays (k_ptrs, v_ptrs, seg_lens, scales) are read during the call only.
+ *   Host arrays (k_ptrs, v_ptrs, seg_lens, scales, key_lens) are read during the call only.
  */
 int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t H, int64_t D,
                        int64_t q_bs, int64_t q_ls, int64_t q_hs, int64_t n_segments,
@@ -222,8 +229,8 @@ int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t H, int64_t 
                        int64_t v_bs, int64_t v_ls, int64_t v_hs, int64_t v_ds, int kv_dtype,
                        const float* const* k_scales, const float* const* v_scales,
                        int64_t sc_bs, int64_t sc_hs, int64_t frame_tokens,
-                       const float* key_mask, int64_t mask_bs, void* out, int64_t o_bs,
-                       int64_t o_ls, int64_t o_hs, float* lse, float scale, void* workspace,
+                       const float* key_mask, int64_t mask_bs, const int64_t* key_lens, void* out,
+                       int64_t o_bs, int64_t o_ls, int64_t o_hs, float* lse, float scale, void* workspace,
                        int64_t workspace_bytes, void* stream);
 
 /*
@@ -248,8 +255,8 @@ int ltx_flash_attn_fwd_noalloc(const void* q, int64_t B, int64_t Lq, int64_t H, 
                                int64_t v_bs, int64_t v_ls, int64_t v_hs, int64_t v_ds, int kv_dtype,
                                const float* const* k_scales, const float* const* v_scales,
                                int64_t sc_bs, int64_t sc_hs, int64_t frame_tokens,
-                               const float* key_mask, int64_t mask_bs, void* out, int64_t o_bs,
-                               int64_t o_ls, int64_t o_hs, float* lse, float scale, void* stream);
+                               const float* key_mask, int64_t mask_bs, const int64_t* key_lens, void* out,
+                               int64_t o_bs, int64_t o_ls, int64_t o_hs, float* lse, float scale, void* stream);
 
 /*
  * Workspace bytes ltx_flash_attn_fwd can use for a [B, Lq, H, D] query on the

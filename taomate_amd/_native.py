@@ -16,8 +16,9 @@ LIB_NAME = "libtaomate_ltx.so"
 
 F32, BF16, F8E4M3 = 0, 1, 2
 MAX_SEGMENTS = 16
+MAX_KEYLEN_BATCH = 16  # LTX_MAX_KEYLEN_BATCH
 NOALLOC_SCRATCH_BYTES = 24 << 20  # LTX_NOALLOC_SCRATCH_BYTES
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
@@ -50,10 +51,10 @@ SIGNATURES = {
                       _ptr, _ptr, _ptr],
     "ltx_flash_attn_fwd": [_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr,
                            _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _ptr, _ptr, _i64, _i64,
-                           _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _ptr, _f32, _ptr, _i64, _ptr],
+                           _i64, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _ptr, _f32, _ptr, _i64, _ptr],
     "ltx_flash_attn_fwd_noalloc": [_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr,
                                    _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _ptr, _ptr, _i64, _i64,
-                                   _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _ptr, _f32, _ptr],
+                                   _i64, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _ptr, _f32, _ptr],
     "ltx_flash_attn_workspace_size": [_i64, _i64, _i64, _i64, _ptr],
     "ltx_adaln": [_i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64,
                   _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _f32, _ptr],

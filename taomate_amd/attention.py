@@ -21,6 +21,7 @@ from typing import Dict, List, Optional, Tuple
 import torch
 import torch.nn as nn
 
+from . import _native as N
 from . import kernels
 from .kernels import KVSegment
 from .kv_cache import KVSpanView, module_arena
@@ -252,28 +253,34 @@ def _key_padding_mask(mask: Optional[torch.Tensor], B: int, Lk: int) -> Optional
     return m.to(torch.float32).contiguous()
 
 
-# A key-padding mask whose kept keys are the same prefix in every batch row,
-# with every other key at or below -1e30 (the reference's (m - 1) * finfo.max
-# form), gives those keys a weight of exactly 0 in float32: attending the
-# prefix alone is the same computation.  The check needs the mask's values on
-# the host, so its result is kept per mask tensor (dropped when the tensor
-# dies, recomputed after an in-place change) and a mask reused across blocks
-# and steps costs one synchronisation.
-_PREFIX: Dict[int, Tuple[int, Optional[int]]] = {}
+# A key-padding mask whose kept keys are a prefix of each batch row, with
+# every other key at or below -1e30 (the reference's (m - 1) * finfo.max form),
+# gives those keys a weight of exactly 0 in float32: attending each row's
+# prefix alone is the same computation.  A prefix common to every row is a
+# shorter key range; prefixes of different lengths are per-row key counts for
+# the pipelined kernel.  The check needs the mask's values on the host, so
+# its result is kept per mask tensor (dropped when the tensor dies, recomputed
+# after an in-place change) and a mask reused across blocks and steps costs
+# one synchronisation.
+_PREFIX: Dict[int, Tuple[int, Optional[Tuple[int, ...]]]] = {}
 
 
-def _kept_prefix(mask: torch.Tensor, km: torch.Tensor) -> Optional[int]:
+def _kept_prefixes(mask: torch.Tensor, km: torch.Tensor) -> Optional[Tuple[int, ...]]:
+    """Per mask row, the length of the kept prefix, when every row keeps a
+    non-empty prefix and drops the rest; else None."""
     key = id(mask)
     hit = _PREFIX.get(key)
     if hit is not None and hit[0] == mask._version:
         return hit[1]
     kept, dropped = km == 0, km <= -1e30
-    n: Optional[int] = None
+    n: Optional[Tuple[int, ...]] = None
     if bool((kept | dropped).all()):
         counts = kept.sum(dim=1)
-        n0 = int(counts[0])
-        if n0 > 0 and bool((counts == n0).all()) and bool(kept[:, :n0].all()):
-            n = n0
+        # a prefix: no kept key after the first dropped one
+        first_drop = torch.where(dropped.any(dim=1), dropped.int().argmax(dim=1),
+                                 torch.full_like(counts, km.shape[1]))
+        if bool((counts == first_drop).all()) and bool((counts > 0).all()):
+            n = tuple(int(c) for c in counts.tolist())
     if hit is None:
         weakref.finalize(mask, _PREFIX.pop, key, None)
     _PREFIX[key] = (mask._version, n)
@@ -312,17 +319,27 @@ def standard_attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
             kk = kk.contiguous()
             vv = vv.contiguous()
     km = _key_padding_mask(mask, B, k.shape[1])
+    key_lens = None
     if km is not None:
-        n = _kept_prefix(mask, km)
-        if n is not None:
+        lens = _kept_prefixes(mask, km)
+        if lens is not None and len(set(lens)) == 1:
+            n = lens[0]
             kk, vv, km = kk[:, :n], vv[:, :n], None
+        elif lens is not None and B <= N.MAX_KEYLEN_BATCH and D in (64, 128) and Lq >= 256:
+            # prefixes of different lengths: per-row key counts on the pipelined
+            # kernel (with fewer queries the masked kernel, whatever V's layout,
+            # so a cached key-major V gives the same result as a fresh one)
+            key_lens, km = lens, None
+            if not key_major:
+                vv = _key_major(vv)
+                key_major = True
     if km is not None and key_major:
         # the masked kernel reads token-major V with K's strides
         kk = kk.contiguous()
         vv = vv.contiguous()
     elif km is None and not key_major and D in (64, 128) and Lq >= 256 and kk.shape[1] >= 64:
         vv = _key_major(vv)
-    kernels.flash_attn(qq, [KVSegment(kk, vv)], out, key_mask=km, scale=scale)
+    kernels.flash_attn(qq, [KVSegment(kk, vv)], out, key_mask=km, scale=scale, key_lens=key_lens)
     return out
 
 

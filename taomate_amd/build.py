@@ -36,6 +36,12 @@ def _run(cmd):
     return out
 
 
+# per-source extra flags: the attention kernels' slot programs are fully
+# unrolled (#pragma unroll) and larger than LLVM's default limit for a
+# requested full unroll (16384), which would leave the fp8 instance rolled
+PER_SOURCE = {"flash_attn.hip": ["-mllvm", "-pragma-unroll-threshold=200000"]}
+
+
 def build(verbose: bool = False) -> pathlib.Path:
     BUILD.mkdir(exist_ok=True)
     LIB.parent.mkdir(exist_ok=True)
@@ -45,7 +51,7 @@ def build(verbose: bool = False) -> pathlib.Path:
     jobs = []
     for src in sources:
         obj = BUILD / (src.stem + ".o")
-        jobs.append((obj, [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]))
+        jobs.append((obj, [HIPCC, *FLAGS, *PER_SOURCE.get(src.name, []), "-c", str(src), "-o", str(obj)]))
     workers = min(len(jobs), max(1, (os.cpu_count() or 2) // 2))
     with cf.ThreadPoolExecutor(workers) as ex:
         outs = list(ex.map(lambda j: _run(j[1]), jobs))

@@ -53,6 +53,11 @@ struct FlashParams {
   int64_t sc_bs, sc_hs;
   int64_t mask_bs;
   int64_t Lk;
+  // per-batch key counts (n_klen == B, or 0 for none): batch row b attends
+  // keys [0, klen[b]) of the concatenated sequence (a key-padding mask that
+  // keeps a prefix of each row)
+  int n_klen;
+  int klen[LTX_MAX_KEYLEN_BATCH];
   int64_t seg_start[LTX_MAX_SEGMENTS + 1];
   const void* k_ptr[LTX_MAX_SEGMENTS];
   const void* v_ptr[LTX_MAX_SEGMENTS];
@@ -179,6 +184,18 @@ struct TileIter {
     key0 += row0;
   }
 };
+
+// Key tiles of the concatenated sequence that hold keys below `lim` (the
+// tiles a batch row with a per-batch key count attends; bf16 tiling).
+__device__ __forceinline__ int tiles_below(const FlashParams& p, int lim) {
+  int t = p.tile_start[p.n_seg];
+  for (int i = p.n_seg - 1; i >= 0; --i)
+    if (lim <= p.seg_start[i + 1]) {
+      const int64_t in = lim - p.seg_start[i];
+      t = p.tile_start[i] + (int)((in > 0 ? in : 0) + kBN - 1) / kBN;
+    }
+  return t;
+}
 
 // Which q-tile and key-tile range block `bid` owns.  Blocks below n_full take
 // whole q-tiles; the rest take 1/split of a tail q-tile's key tiles.  Each
@@ -676,9 +693,8 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 //
 // * P = 2^(S*c - m) (c = scale*log2 e) is one v_fma and one v_exp per score:
 //   no tile maximum is taken on the common path.
-// * The row sum comes from v_dot2c_f32_bf16 over the packed bf16 P (two keys
-//   per instruction) and doubles as the overflow check: m is not raised every
-//   tile.  While the per-lane sum of a tile stays at or below 2^16, every P
+// * The row sum (fp32 adds of the P values) doubles as the overflow check:
+//   m is not raised every tile.  While the per-lane sum of a tile stays at or below 2^16, every P
 //   of that tile is at most 2^16, which fp32 sums and bf16 P carry as exactly
 //   as P <= 1.  When a lane's sum goes above it, the tile maximum is taken
 //   and m, O and l are rescaled before P is redone (the online normaliser of
@@ -717,10 +733,11 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 template <bool FRAMED>
 struct KeyStreamT {
   int s, rem, frem;
+  int lim = 0x7FFFFFFF;  // keys past this index of the concatenated sequence are not part of the stream
   const char* ptr;
   __device__ __forceinline__ void enter(const void* const* base, int64_t head, const FlashParams& p, int seg) {
     s = seg;
-    rem = (int)(p.seg_start[seg + 1] - p.seg_start[seg]);
+    rem = (int)((p.seg_start[seg + 1] < lim ? p.seg_start[seg + 1] : (int64_t)lim) - p.seg_start[seg]);
     ptr = reinterpret_cast<const char*>(base[seg]) + head;
     if constexpr (FRAMED) frem = p.frame;
   }
@@ -815,7 +832,15 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
   const int lane = threadIdx.x & 63;
   const int li = lane & 31, hg = lane >> 5;
   const int qi = qt * BM + wave * 32 + li;
-  const int ntiles = wi.j1 - wi.j0;
+  // a per-batch key count ends this row's key tiles early (the streams stop
+  // at it, so its last tile is partial and masked like a segment's last)
+  const int klim = (!FP8 && p.n_klen) ? p.klen[b] : 0x7FFFFFFF;
+  int jend = wi.j1;
+  if (!FP8 && p.n_klen) {
+    const int tb = tiles_below(p, klim);
+    jend = jend < tb ? jend : tb;
+  }
+  const int ntiles = jend > wi.j0 ? jend - wi.j0 : 0;
 
   // ---- per-lane load offsets (bytes from a tile's first key), loop invariant ----
   const int row_bytes = (int)(p.kv_ls * (FP8 ? 1 : 2));
@@ -852,6 +877,8 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
   const int64_t k_tile = (int64_t)BN * row_bytes;
   const int64_t v_tile = FP8 ? k_tile : BN * 2;
   KeyStreamT<FRAMED> kit, vit;
+  kit.lim = klim;
+  vit.lim = klim;
   kit.seek(p.k_ptr, k_head, k_tile, p, wi.j0);
   vit.seek(p.v_ptr, v_head, v_tile, p, wi.j0);
   // LDS address of this wave's first load slot in a buffer; the empty asm
@@ -1080,7 +1107,11 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
   // values: v_dot2c_f32_bf16 over the packed pair (one instruction instead
   // of two) waits for the SIMD's matrix pipeline on gfx950, about one MFMA
   // per instruction while the other wave's MFMAs run, where adds issue
-  // beside them (bf16 instances; fp8 keeps the dot2).
+  // beside them (fp8 at 1152 x 4608: 199.0 -> 191.0 us with the adds).
+  // The fully unrolled slot program of the fp8 instances is larger than
+  // LLVM's default limit for a pragma-requested full unroll; the library is
+  // built with a higher one (-pragma-unroll-threshold), without which the
+  // loop stays rolled and its per-slot arrays go to scratch memory.
   constexpr int NS = 4 * DB + 2 * QS;
   constexpr int PREF = 3;
   // fp8 staging inside the slot program: one unit (a K row chunk, a V half,
@@ -1134,18 +1165,12 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
         if ((2 * q * NS) / 32 + 3 == t || (q == 15 && t == NS + 1 && (2 * q * NS) / 32 + 3 > NS + 1)) {
           pcur[q] = pack_bf16x2(e0[q], e1[q]);
           float& ps = (q & 1) ? ps1 : ps0;
-          if constexpr (FP8) {
-            // the fp8 instances keep the packed dot2 (their staging
-            // registers leave no room for the adds' live ranges)
-            ps = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(ltx_bf16x2_t, pcur[q]), ones, ps, false);
-          } else {
-            ps = ps + e0[q];
-            ps = ps + e1[q];
-            // with no use left in this slot the compiler would sink the pack
-            // to the next tile's PV and issue all sixteen back to back after
-            // the slot program; pin it here, under this slot's MFMA
-            asm volatile("" : "+v"(pcur[q]));
-          }
+          ps = ps + e0[q];
+          ps = ps + e1[q];
+          // with no use left in this slot the compiler would sink the pack
+          // to the next tile's PV and issue all sixteen back to back after
+          // the slot program; pin it here, under this slot's MFMA
+          asm volatile("" : "+v"(pcur[q]));
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -1454,8 +1479,8 @@ static int flash_attn_fwd_impl(const void* q, int64_t B, int64_t Lq, int64_t H, 
                                int64_t v_bs, int64_t v_ls, int64_t v_hs, int64_t v_ds, int kv_dtype,
                                const float* const* k_scales, const float* const* v_scales,
                                int64_t sc_bs, int64_t sc_hs, int64_t frame_tokens,
-                               const float* key_mask, int64_t mask_bs, void* out, int64_t o_bs,
-                               int64_t o_ls, int64_t o_hs, float* lse, float scale,
+                               const float* key_mask, int64_t mask_bs, const int64_t* key_lens, void* out,
+                               int64_t o_bs, int64_t o_ls, int64_t o_hs, float* lse, float scale,
                                void* workspace, int64_t workspace_bytes, bool strict_ws, void* stream) {
   LTX_REQUIRE(q && out, "ltx_flash_attn_fwd: null q/out");
   LTX_REQUIRE(D == 64 || D == 128, "ltx_flash_attn_fwd: head dim %lld unsupported (64 or 128)",
@@ -1537,6 +1562,19 @@ static int flash_attn_fwd_impl(const void* q, int64_t B, int64_t Lq, int64_t H, 
   p.n_seg = n;
   p.Lk = p.seg_start[n];
   if (key_mask) LTX_REQUIRE(!fp8, "ltx_flash_attn_fwd: key mask with fp8 KV is not built");
+  if (key_lens) {
+    LTX_REQUIRE(vkey && !fp8 && key_mask == nullptr,
+                "ltx_flash_attn_fwd: key_lens needs bf16 key-major V and no key mask");
+    LTX_REQUIRE(B <= LTX_MAX_KEYLEN_BATCH, "ltx_flash_attn_fwd: key_lens supports at most %d batch rows",
+                LTX_MAX_KEYLEN_BATCH);
+    for (int64_t b = 0; b < B; ++b) {
+      LTX_REQUIRE(key_lens[b] >= 0 && key_lens[b] <= p.Lk,
+                  "ltx_flash_attn_fwd: key_lens[%lld] = %lld outside [0, %lld]", (long long)b,
+                  (long long)key_lens[b], (long long)p.Lk);
+      p.klen[b] = (int)key_lens[b];
+    }
+    p.n_klen = (int)B;
+  }
   LTX_REQUIRE(k_ls * esz * kBN < (int64_t)1 << 31 && k_ls >= D,
               "ltx_flash_attn_fwd: kv token stride %lld out of range", (long long)k_ls);
   p.n_qtiles = (int)((Lq + kBM - 1) / kBM);
@@ -1606,14 +1644,14 @@ extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t 
                                   int64_t v_bs, int64_t v_ls, int64_t v_hs, int64_t v_ds, int kv_dtype,
                                   const float* const* k_scales, const float* const* v_scales,
                                   int64_t sc_bs, int64_t sc_hs, int64_t frame_tokens,
-                                  const float* key_mask, int64_t mask_bs, void* out, int64_t o_bs,
-                                  int64_t o_ls, int64_t o_hs, float* lse, float scale,
+                                  const float* key_mask, int64_t mask_bs, const int64_t* key_lens, void* out,
+                                  int64_t o_bs, int64_t o_ls, int64_t o_hs, float* lse, float scale,
                                   void* workspace, int64_t workspace_bytes, void* stream) {
   clear_error();
   return flash_attn_fwd_impl(q, B, Lq, H, D, q_bs, q_ls, q_hs, n_segments, k_ptrs, v_ptrs, seg_lens, k_bs,
                              k_ls, k_hs, v_bs, v_ls, v_hs, v_ds, kv_dtype, k_scales, v_scales, sc_bs, sc_hs,
-                             frame_tokens, key_mask, mask_bs, out, o_bs, o_ls, o_hs, lse, scale, workspace,
-                             workspace_bytes, false, stream);
+                             frame_tokens, key_mask, mask_bs, key_lens, out, o_bs, o_ls, o_hs, lse, scale,
+                             workspace, workspace_bytes, false, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -1666,13 +1704,13 @@ extern "C" int ltx_flash_attn_fwd_noalloc(const void* q, int64_t B, int64_t Lq, 
                                           int kv_dtype, const float* const* k_scales,
                                           const float* const* v_scales, int64_t sc_bs, int64_t sc_hs,
                                           int64_t frame_tokens, const float* key_mask, int64_t mask_bs,
-                                          void* out, int64_t o_bs, int64_t o_ls, int64_t o_hs, float* lse,
-                                          float scale, void* stream) {
+                                          const int64_t* key_lens, void* out, int64_t o_bs, int64_t o_ls,
+                                          int64_t o_hs, float* lse, float scale, void* stream) {
   clear_error();
   void* ws = scratch_for_current_device();
   if (ws == nullptr) return LTX_ELAUNCH;
   return flash_attn_fwd_impl(q, B, Lq, H, D, q_bs, q_ls, q_hs, n_segments, k_ptrs, v_ptrs, seg_lens, k_bs,
                              k_ls, k_hs, v_bs, v_ls, v_hs, v_ds, kv_dtype, k_scales, v_scales, sc_bs, sc_hs,
-                             frame_tokens, key_mask, mask_bs, out, o_bs, o_ls, o_hs, lse, scale, ws,
+                             frame_tokens, key_mask, mask_bs, key_lens, out, o_bs, o_ls, o_hs, lse, scale, ws,
                              kScratchBytes, true, stream);
 }

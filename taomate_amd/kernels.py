@@ -264,8 +264,11 @@ class KVSegment:
 
 def flash_attn(q: torch.Tensor, segments: List[KVSegment], out: torch.Tensor,
                key_mask: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
-               scale: Optional[float] = None, frame_tokens: int = 0, noalloc: bool = False) -> None:
+               scale: Optional[float] = None, frame_tokens: int = 0, noalloc: bool = False,
+               key_lens: Optional[Sequence[int]] = None) -> None:
     """ltx_flash_attn_fwd.  q/out [B, Lq, H, D] bf16; key_mask float32 [B, Lk] additive.
+    ``key_lens`` (B host ints): batch row b attends keys [0, key_lens[b]) only
+    (a prefix-per-row padding mask, bf16 key-major V, on the pipelined kernel).
     ``noalloc`` calls ltx_flash_attn_fwd_noalloc instead: no workspace tensor,
     the split partials go to the library's fixed per-device scratch array
     (calls overlapping on one device race on it)."""
@@ -326,6 +329,11 @@ def flash_attn(q: torch.Tensor, segments: List[KVSegment], out: torch.Tensor,
         mask_bs = 0 if key_mask.shape[0] == 1 else key_mask.stride(0)
     if lse is not None and (lse.dtype != torch.float32 or lse.shape != (B, H, Lq) or not lse.is_contiguous()):
         raise ValueError("flash_attn: lse must be contiguous float32 [B, H, Lq]")
+    kl = None
+    if key_lens is not None:
+        if len(key_lens) != B or any(not 0 <= int(n) <= lk for n in key_lens):
+            raise ValueError(f"flash_attn: key_lens must hold {B} counts in [0, {lk}]")
+        kl = N.i64_array([int(n) for n in key_lens])
     kp = N.ptr_array([s.k.data_ptr() for s in segs])
     vp = N.ptr_array([s.v.data_ptr() for s in segs])
     lens = N.i64_array([s.k.shape[1] for s in segs])
@@ -337,7 +345,8 @@ def flash_attn(q: torch.Tensor, segments: List[KVSegment], out: torch.Tensor,
             kv_code,
             ctypes.cast(ksp, ctypes.c_void_p) if fp8 else None,
             ctypes.cast(vsp, ctypes.c_void_p) if fp8 else None, sc_bs, sc_hs,
-            int(frame_tokens), _ptr(key_mask), mask_bs, out.data_ptr(), out.stride(0), out.stride(1),
+            int(frame_tokens), _ptr(key_mask), mask_bs,
+            ctypes.cast(kl, ctypes.c_void_p) if kl is not None else None, out.data_ptr(), out.stride(0), out.stride(1),
             out.stride(2), _ptr(lse), float(scale) if scale is not None else 0.0)
     if noalloc:
         N.call("ltx_flash_attn_fwd_noalloc", *args, _stream(q))

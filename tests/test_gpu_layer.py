@@ -339,9 +339,10 @@ def test_denoise_steps_do_not_commit(dev):
 @pytest.mark.parametrize("kind", ["common_prefix", "per_row_prefix", "holes", "soft_bias", "bool_prefix"])
 def test_standard_attention_mask_forms(dev, kind):
     """Key-padding masks through standard_attention_forward: a prefix kept in
-    every row is attended as the prefix alone (pipelined kernel on a key-major
-    V copy); other forms (row-dependent prefixes, holes, finite biases) take the
-    masked kernel.  All against the oracle with the same additive mask."""
+    every row is attended as the prefix alone and row-dependent prefixes as
+    per-row key counts (both on the pipelined kernel over a key-major V copy);
+    other forms (holes, finite biases) take the masked kernel.  All against
+    the oracle with the same additive mask."""
     B, Lq, Lk, H, D = 2, 384, 700, 8, 128
     g = torch.Generator().manual_seed(61)
     q = torch.randn(B, Lq, H, D, generator=g).to(torch.bfloat16)
@@ -369,3 +370,75 @@ def test_standard_attention_mask_forms(dev, kind):
     assert_bf16_close(out, ref, kind)
     assert torch.equal(out, again)
     assert cosine(out, ref) >= 0.9999
+
+
+def test_text_cross_per_row_prefixes_take_the_pipelined_kernel(dev, monkeypatch):
+    """Cond / uncond prompts of different lengths: 1152 queries against 1024
+    text keys (32 x 128) with batch row 0 keeping 1024 keys and row 1 keeping
+    700 (the reference's additive mask, causal_model.py:551-562, applied at
+    kv_cache.py:764-827).  The call goes to the pipelined kernel with per-row
+    key counts (no float mask, key-major V) and matches the oracle."""
+    from taomate_amd import kernels as K
+    B, Lq, Lk, H, D = 2, 1152, 1024, 32, 128
+    g = torch.Generator().manual_seed(67)
+    q = torch.randn(B, Lq, H, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Lk, H, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Lk, H, D, generator=g).to(torch.bfloat16)
+    keep = torch.ones(B, Lk, dtype=torch.int64)
+    keep[1, 700:] = 0
+    add = OA.prepare_attention_mask(keep, torch.bfloat16)
+    ref = OA.standard_attention_forward(q.float(), k.float(), v.float(), add.float())
+    seen = []
+    real = K.flash_attn
+
+    def spy(qq, segs, out, **kw):
+        seen.append((kw.get("key_mask"), kw.get("key_lens"), segs[0].v.stride(1)))
+        return real(qq, segs, out, **kw)
+
+    monkeypatch.setattr(K, "flash_attn", spy)
+    with torch.no_grad():
+        out = T.standard_attention_forward(q.to(dev), k.to(dev), v.to(dev), mask=add.to(dev))
+    torch.cuda.synchronize()
+    assert len(seen) == 1 and seen[0][0] is None and tuple(seen[0][1]) == (1024, 700) and seen[0][2] == 1
+    assert_bf16_close(out, ref, "per-row prefixes")
+    assert cosine(out, ref) >= 0.9999
+
+
+@pytest.mark.parametrize("Lq", [1152, 1024, 300], ids=["split_tail", "pair", "one_round"])
+def test_flash_attn_key_lens_over_segments(dev, Lq):
+    """ltx_flash_attn_fwd's key_lens over two key-major segments: row 0 stops
+    inside the first segment (mid-tile), row 1 inside the second; the split
+    tail (1152 queries), the pair kernel (1024) and a single round (300)
+    against the oracle attending each row's keys alone."""
+    from taomate_amd import kernels as K
+    from taomate_amd.attention import _key_major
+    B, H, D = 2, 32, 128
+    L1, L2 = 1000, 1500
+    lens = (613, 1000 + 877)
+    g = torch.Generator().manual_seed(71)
+    q = torch.randn(B, Lq, H, D, generator=g).to(torch.bfloat16)
+    kc = torch.randn(B, L1 + L2, H, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(B, L1 + L2, H, D, generator=g).to(torch.bfloat16)
+    kd, vd = kc.to(dev), _key_major(vc.to(dev))     # segments share strides: views of one store
+    segs = [K.KVSegment(kd[:, :L1], vd[:, :L1]), K.KVSegment(kd[:, L1:], vd[:, L1:])]
+    out = torch.empty(B, Lq, H, D, device=dev, dtype=torch.bfloat16)
+    K.flash_attn(q.to(dev), segs, out, key_lens=lens)
+    torch.cuda.synchronize()
+    for b in range(B):
+        n = lens[b]
+        ref = OA.standard_attention_forward(q[b:b + 1].float(), kc[b:b + 1, :n].float(), vc[b:b + 1, :n].float())
+        assert_bf16_close(out[b:b + 1], ref, f"row {b} keeps {n}")
+        assert cosine(out[b:b + 1], ref) >= 0.9999
+
+
+def test_flash_attn_key_lens_rejections(dev):
+    from taomate_amd import kernels as K
+    q = torch.zeros(2, 128, 8, 128, device=dev, dtype=torch.bfloat16)
+    k = torch.zeros(2, 64, 8, 128, device=dev, dtype=torch.bfloat16)
+    out = torch.empty_like(q)
+    with pytest.raises(ValueError, match="key_lens"):
+        K.flash_attn(q, [K.KVSegment(k, k)], out, key_lens=(64, 65))
+    # token-major V: the entry point refuses per-row counts
+    from taomate_amd import _native as N
+    with pytest.raises(N.NativeCallError, match="key_lens"):
+        K.flash_attn(q, [K.KVSegment(k, k.clone())], out, key_lens=(64, 10))

@@ -180,7 +180,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(lib, n), n
         assert n in _native.SIGNATURES, n
-    assert lib.ltx_abi_version() == 1
+    assert lib.ltx_abi_version() == _native.ABI_VERSION == 2
 
 
 def test_abi_rejects_bad_arguments_without_a_gpu():
@@ -188,7 +188,7 @@ def test_abi_rejects_bad_arguments_without_a_gpu():
     rc = lib.ltx_rope_table(None, None, 1, None, 0, 3, 1, 1, 1, 0, 0, 20.0, 2048.0, 2048.0, 64, 1, 1, None)
     assert rc == -1 and b"null pointer" in lib.ltx_last_error()
     rc = lib.ltx_flash_attn_fwd(ctypes.c_void_p(16), 1, 1, 1, 96, 0, 0, 0, 0, None, None, None, 0, 0, 0,
-                                0, 0, 0, 1, 1, None, None, 0, 0, 0, None, 0, ctypes.c_void_p(16), 0, 0,
+                                0, 0, 0, 1, 1, None, None, 0, 0, 0, None, 0, None, ctypes.c_void_p(16), 0, 0,
                                 0, None, 0.0, None, 0, None)
     assert rc == -1 and b"head dim" in lib.ltx_last_error()
     rc = lib.ltx_kv_gather(3, 1, 1, 8, None, 0, 0, 0, None, 0, 0, 0, 0, None, None, None)
@@ -202,7 +202,7 @@ def test_abi_rejects_bad_arguments_without_a_gpu():
     assert rc == -1 and b"null pointer" in lib.ltx_last_error()
     with pytest.raises(_native.NativeCallError, match="n_segments"):
         _native.call("ltx_flash_attn_fwd", ctypes.c_void_p(16), 1, 1, 1, 128, 0, 0, 0, 17, None, None,
-                     None, 0, 0, 0, 0, 0, 0, 1, 1, None, None, 0, 0, 0, None, 0, ctypes.c_void_p(16), 0,
+                     None, 0, 0, 0, 0, 0, 0, 1, 1, None, None, 0, 0, 0, None, 0, None, ctypes.c_void_p(16), 0,
                      0, 0, None, 0.0, None, 0, None)
 
 

@@ -70,6 +70,23 @@ int ltx_rope_table(void* cos_out, void* sin_out, int out_dtype, const float* fre
                    int64_t batch, void* stream);
 
 /*
+ * The SPLIT video (3-D) table of ltx_rope_table for a new start frame, from a
+ * table of the same grid, dim, heads and frequencies built for any other start
+ * frame (also causal_precompute_freqs_cis, causal_rope.py:139-357: the same
+ * values, built another way).  Only the t-axis entries depend on the start
+ * frame (causal_rope.py:264-267, 284-288); the h, w and pad entries are read
+ * from the source table.  Every entry is bit-identical to ltx_rope_table's.
+ *   cos_out/sin_out, cos_src/sin_src: [1, H, T, dim/(2H)], T = grid_f *
+ *   grid_h * grid_w, 16-byte aligned, dim/(2H) entries a multiple of 16 bytes;
+ *   the source and output must not overlap.
+ *   max_pos_t: the time normaliser (reference default 20).
+ */
+int ltx_rope_table_retime(void* cos_out, void* sin_out, const void* cos_src, const void* sin_src,
+                          int out_dtype, const float* freq_idx, int64_t n_freq, int64_t grid_f,
+                          int64_t grid_h, int64_t grid_w, int64_t start_frame, float max_pos_t,
+                          int64_t dim, int64_t num_heads, void* stream);
+
+/*
  * Fused full-row RMSNorm + SPLIT RoPE on q and k rows.
  * Replaces, in order: q_norm/k_norm = nn.RMSNorm(H*D, eps)
  * (ltx_causal/attention/causal_attention.py:105-106, applied at

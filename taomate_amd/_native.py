@@ -31,6 +31,8 @@ SIGNATURES = {
     "ltx_last_error": [],
     "ltx_rope_table": [_ptr, _ptr, _int, _ptr, _i64, _int, _i64, _i64, _i64, _i64, _int, _f32, _f32,
                        _f32, _i64, _i64, _i64, _ptr],
+    "ltx_rope_table_retime": [_ptr, _ptr, _ptr, _ptr, _int, _ptr, _i64, _i64, _i64, _i64, _i64, _f32, _i64, _i64,
+                              _ptr],
     "ltx_qk_rmsnorm_rope": [_int, _i64, _i64, _i64,
                             _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _f32, _ptr, _ptr, _i64,
                             _i64, _i64,

@@ -188,6 +188,71 @@ __global__ void __launch_bounds__(256) rope_table_video_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// The video table of a new start frame from a table of the same grid (any
+// start frame).  Only the t-axis entries depend on the start frame: the h and
+// w entries of token (f, r, c) are those of (r, c) in every frame, and the pad
+// entries are the identity.  One workgroup per (frame, head, block of
+// kRopeRows rows) computes its frame's t-axis cos/sin with the float32
+// operations of rope_table_kernel (so every entry is bit-identical to a fresh
+// build) and streams the rows: 16-byte loads of the source entries, the
+// t-axis ones replaced, 16-byte stores.  A long stream builds one 3-frame
+// table per chunk; this reads and writes it instead of evaluating the h and w
+// angles again.
+// ---------------------------------------------------------------------------
+template <typename TOut>
+__global__ void __launch_bounds__(256) rope_table_retime_kernel(
+    TOut* __restrict__ cos_out, TOut* __restrict__ sin_out, const TOut* __restrict__ cos_src,
+    const TOut* __restrict__ sin_src, const float* __restrict__ freq_idx, int n_freq, int grid_h, int grid_w,
+    int64_t start_frame, float max_t, int half_dim, int heads, int64_t T) {
+  extern __shared__ float tfac[];  // [P][2]: this frame's t-axis cos / sin (other entries unused)
+  const int f = blockIdx.x, h = blockIdx.y;
+  const int r0 = blockIdx.z * kRopeRows;
+  const int nr = min(kRopeRows, grid_h - r0);
+  const int P = half_dim / heads;
+  const int pad = half_dim - n_freq * 3;
+  for (int j = threadIdx.x; j < P; j += blockDim.x) {
+    const int g = h * P + j;
+    float c = 1.0f, sn = 0.0f;
+    if (g >= pad && (g - pad) % 3 == 0) {
+      const int fi = (g - pad) / 3;
+      const float frac = video_frac(0, start_frame + f, max_t, 1.0f, 1.0f);
+      const float ang = __fmul_rn(freq_idx[fi], __fadd_rn(__fmul_rn(frac, 2.0f), -1.0f));
+      c = cosf(ang);
+      sn = sinf(ang);
+    }
+    tfac[2 * j] = c;
+    tfac[2 * j + 1] = sn;
+  }
+  __syncthreads();
+  constexpr int V = 16 / sizeof(TOut);  // entries per 16-byte vector
+  const int64_t t0 = (int64_t)f * grid_h * grid_w + (int64_t)r0 * grid_w;
+  const int PV = P / V;
+  for (int e = threadIdx.x; e < nr * grid_w * PV; e += blockDim.x) {
+    const int tl = e / PV, j0 = (e % PV) * V;
+    const int64_t o = ((int64_t)h * T + t0 + tl) * P + j0;
+    uint4 cv = *reinterpret_cast<const uint4*>(cos_src + o);
+    uint4 sv = *reinterpret_cast<const uint4*>(sin_src + o);
+    TOut* ce = reinterpret_cast<TOut*>(&cv);
+    TOut* se = reinterpret_cast<TOut*>(&sv);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const int g = h * P + j0 + i;
+      if (g >= pad && (g - pad) % 3 == 0) {
+        if constexpr (sizeof(TOut) == 2) {
+          ce[i] = f32_to_bf16_bits(tfac[2 * (j0 + i)]);
+          se[i] = f32_to_bf16_bits(tfac[2 * (j0 + i) + 1]);
+        } else {
+          ce[i] = tfac[2 * (j0 + i)];
+          se[i] = tfac[2 * (j0 + i) + 1];
+        }
+      }
+    }
+    *reinterpret_cast<uint4*>(cos_out + o) = cv;
+    *reinterpret_cast<uint4*>(sin_out + o) = sv;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Fused RMSNorm + SPLIT RoPE.  Block = (H*D)/16 threads; thread (h, c) owns the
 // 8 elements [c*8, c*8+8) of head h's first half and the matching 8 of its
 // second half, i.e. the 8 (x1, x2) rotation pairs j = c*8 .. c*8+7.
@@ -609,6 +674,42 @@ int norm_setup(int dtype, int64_t B, int64_t H, int64_t D,
 }
 
 }  // namespace
+
+extern "C" int ltx_rope_table_retime(void* cos_out, void* sin_out, const void* cos_src, const void* sin_src,
+                                     int out_dtype, const float* freq_idx, int64_t n_freq, int64_t grid_f,
+                                     int64_t grid_h, int64_t grid_w, int64_t start_frame, float max_pos_t,
+                                     int64_t dim, int64_t num_heads, void* stream) {
+  clear_error();
+  LTX_REQUIRE(cos_out && sin_out && cos_src && sin_src && freq_idx, "ltx_rope_table_retime: null pointer");
+  LTX_REQUIRE(out_dtype == LTX_F32 || out_dtype == LTX_BF16, "ltx_rope_table_retime: out_dtype must be F32 or BF16");
+  LTX_REQUIRE(dim > 0 && dim % 2 == 0 && num_heads > 0 && num_heads <= 65535 && (dim / 2) % num_heads == 0,
+              "ltx_rope_table_retime: dim/2 must be divisible by num_heads");
+  LTX_REQUIRE(n_freq >= 0 && n_freq * 3 <= dim / 2, "ltx_rope_table_retime: n_freq*3 exceeds dim/2");
+  LTX_REQUIRE(grid_f >= 0 && grid_f <= 0x7FFFFFFF && grid_h > 0 && grid_w > 0, "ltx_rope_table_retime: bad grid");
+  const int half = (int)(dim / 2);
+  const int P = half / (int)num_heads;
+  const int64_t esz = out_dtype == LTX_BF16 ? 2 : 4;
+  LTX_REQUIRE((P * esz) % 16 == 0, "ltx_rope_table_retime: dim/(2 heads) entries must fill 16-byte vectors");
+  auto al = [](const void* ptr) { return ((uintptr_t)ptr % 16) == 0; };
+  LTX_REQUIRE(al(cos_out) && al(sin_out) && al(cos_src) && al(sin_src),
+              "ltx_rope_table_retime: tables must be 16-byte aligned");
+  LTX_REQUIRE(grid_h * grid_w <= 0x7FFFFFFF / P, "ltx_rope_table_retime: grid too large");
+  const int64_t T = grid_f * grid_h * grid_w;
+  if (T == 0) return LTX_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 vgrid((unsigned)grid_f, (unsigned)num_heads, (unsigned)ceil_div(grid_h, kRopeRows));
+  const size_t lds = (size_t)P * 2 * sizeof(float);
+  if (out_dtype == LTX_BF16)
+    hipLaunchKernelGGL(rope_table_retime_kernel<uint16_t>, vgrid, dim3(256), lds, st, (uint16_t*)cos_out,
+                       (uint16_t*)sin_out, (const uint16_t*)cos_src, (const uint16_t*)sin_src, freq_idx,
+                       (int)n_freq, (int)grid_h, (int)grid_w, start_frame, max_pos_t, half, (int)num_heads, T);
+  else
+    hipLaunchKernelGGL(rope_table_retime_kernel<float>, vgrid, dim3(256), lds, st, (float*)cos_out,
+                       (float*)sin_out, (const float*)cos_src, (const float*)sin_src, freq_idx, (int)n_freq,
+                       (int)grid_h, (int)grid_w, start_frame, max_pos_t, half, (int)num_heads, T);
+  LTX_LAUNCH_CHECK("ltx_rope_table_retime");
+  return LTX_OK;
+}
 
 extern "C" int ltx_qk_rmsnorm_rope(int dtype, int64_t B, int64_t H, int64_t D,
                                    const void* q_in, int64_t q_len, int64_t q_in_bs, int64_t q_in_ls,

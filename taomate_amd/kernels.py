@@ -57,6 +57,26 @@ def rope_table(freq_idx: torch.Tensor, grid: Tuple[int, ...], start_frame: int, 
     return cos, sin
 
 
+def rope_table_retime(src: Tuple[torch.Tensor, torch.Tensor], freq_idx: torch.Tensor, grid: Tuple[int, int, int],
+                      start_frame: int, max_pos_t: float, dim: int, num_heads: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """ltx_rope_table_retime: the video table of ``grid`` at ``start_frame``
+    from ``src`` = (cos, sin) [1, H, T, dim/(2H)] of the same grid built for
+    another start frame."""
+    cs, ss = src
+    _need_gpu(freq_idx, cs, ss)
+    T = math.prod(grid)
+    per = dim // 2 // num_heads
+    for t in (cs, ss):
+        if t.shape != (1, num_heads, T, per) or not t.is_contiguous() or t.dtype != cs.dtype:
+            raise ValueError(f"rope_table_retime: source tables must be contiguous [1, {num_heads}, {T}, {per}]")
+    cos = torch.empty_like(cs)
+    sin = torch.empty_like(ss)
+    N.call("ltx_rope_table_retime", cos.data_ptr(), sin.data_ptr(), cs.data_ptr(), ss.data_ptr(), _code(cos),
+           freq_idx.data_ptr(), freq_idx.numel(), grid[0], grid[1], grid[2], int(start_frame), float(max_pos_t),
+           dim, num_heads, _stream(freq_idx))
+    return cos, sin
+
+
 def _rows(t: torch.Tensor, HD: int) -> Tuple[int, int, int]:
     """(len, b_stride, l_stride) of a [B, L, H*D] (or [B, L, H, D]) row tensor."""
     if t.dim() == 4:

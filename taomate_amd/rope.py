@@ -32,6 +32,10 @@ class CausalRopeType(Enum):
 _FREQ_CACHE: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
 _TABLE_CACHE: "OrderedDict[tuple, Tuple[torch.Tensor, torch.Tensor]]" = OrderedDict()
 _TABLE_CACHE_SIZE = 16
+# one built video table per layout (everything but the start frame, with the
+# theta actually used): a table for a new start frame is derived from it by
+# ltx_rope_table_retime, which recomputes only the t-axis entries
+_VIDEO_TEMPLATES: "OrderedDict[tuple, Tuple[torch.Tensor, torch.Tensor]]" = OrderedDict()
 
 
 def generate_freq_grid(theta: float, max_pos_count: int, inner_dim: int,
@@ -126,8 +130,20 @@ def causal_precompute_freqs_cis(
     # the batch dimension is a stride-0 expansion: the values are the
     # reference's [B, H, T, dim/(2H)] tables, and the kernels that read them
     # see one copy (shared through the cache hierarchy) instead of B
-    cos, sin = kernels.rope_table(freq, grid, start_frame, is_audio, [float(m) for m in max_pos[:nd]],
-                                  dim, num_attention_heads, 1, dtype)
+    tkey = (grid, int(dim), float(th), tuple(int(m) for m in max_pos[:nd]), str(dev), str(dtype),
+            int(num_attention_heads)) if nd == 3 else None
+    tmpl = _VIDEO_TEMPLATES.get(tkey) if tkey is not None else None
+    per = dim // 2 // num_attention_heads
+    if tmpl is not None:
+        cos, sin = kernels.rope_table_retime(tmpl, freq, grid, start_frame, float(max_pos[0]), dim,
+                                             num_attention_heads)
+    else:
+        cos, sin = kernels.rope_table(freq, grid, start_frame, is_audio, [float(m) for m in max_pos[:nd]],
+                                      dim, num_attention_heads, 1, dtype)
+        if tkey is not None and (per * cos.element_size()) % 16 == 0:
+            _VIDEO_TEMPLATES[tkey] = (cos, sin)
+            while len(_VIDEO_TEMPLATES) > _TABLE_CACHE_SIZE:
+                _VIDEO_TEMPLATES.popitem(last=False)
     out = (cos.expand(batch, -1, -1, -1), sin.expand(batch, -1, -1, -1))
     _TABLE_CACHE[key] = out
     while len(_TABLE_CACHE) > _TABLE_CACHE_SIZE:

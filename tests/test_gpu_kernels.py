@@ -52,6 +52,36 @@ def test_rope_table_matches_oracle(dev, case):
     assert u.max() <= 1 and (u == 0).mean() >= 0.999
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+@pytest.mark.parametrize("grid,dim,heads", [((3, 16, 24), 4096, 32), ((2, 8, 12), 512, 8), ((2, 18, 20), 4096, 32)],
+                         ids=["16x24_32x128", "8x12_8x64", "18x20"])
+def test_rope_table_retime_bit_identical(dev, grid, dim, heads, dtype):
+    """A video table derived for a new start frame from one built for another
+    (ltx_rope_table_retime: h, w and pad entries copied, t entries recomputed)
+    equals the table built directly for that frame bit for bit, for start
+    frames around the causal clamp (0, 1) and far along a stream; and
+    causal_precompute_freqs_cis, which derives every table after the first of
+    a layout, returns those tables."""
+    from taomate_amd import kernels as K
+    from taomate_amd import rope as R
+    mp = [20.0, 2048.0, 2048.0]
+    freq = generate_freq_grid(10000.0, 3, dim, dev)
+    src = K.rope_table(freq, grid, 5, False, mp, dim, heads, 1, dtype)
+    for sf in (0, 1, 5, 13, 186, 4000):
+        want = K.rope_table(freq, grid, sf, False, mp, dim, heads, 1, dtype)
+        got = K.rope_table_retime(src, freq, grid, sf, mp[0], dim, heads)
+        assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1]), sf
+    R._TABLE_CACHE.clear()
+    R._VIDEO_TEMPLATES.clear()
+    gs = torch.tensor([list(grid)] * 2)
+    for sf in (3, 9, 4000):
+        cos, sin = causal_precompute_freqs_cis(gs, dim, start_frame=sf, device=dev, dtype=dtype,
+                                               num_attention_heads=heads)
+        want = K.rope_table(freq, grid, sf, False, mp, dim, heads, 1, dtype)
+        assert cos.shape[0] == 2 and torch.equal(cos[1], want[0][0]) and torch.equal(sin[0], want[1][0]), sf
+    assert len(R._VIDEO_TEMPLATES) == 1
+
+
 def test_freq_grid_is_reference_expression(dev):
     f = generate_freq_grid(10000.0, 3, 4096, dev).cpu()
     assert torch.equal(f, OR.generate_freq_grid(10000.0, 3, 4096))

@@ -115,6 +115,7 @@ def _cpu_kernels(monkeypatch):
             n_out.copy_(x)
 
     monkeypatch.setattr(kernels, "rope_table", rope_table)
+    monkeypatch.setattr(kernels, "rope_table_retime", lambda src, *a, **k: (src[0].clone(), src[1].clone()))
     monkeypatch.setattr(kernels, "qk_rmsnorm_rope", qk)
     monkeypatch.setattr(kernels, "flash_attn", lambda q, segs, out, **kw: out.zero_())
     monkeypatch.setattr(kernels, "adaln", adaln)

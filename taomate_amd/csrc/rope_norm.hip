@@ -210,6 +210,24 @@ __global__ void __launch_bounds__(256) rope_table_retime_kernel(
   const int nr = min(kRopeRows, grid_h - r0);
   const int P = half_dim / heads;
   const int pad = half_dim - n_freq * 3;
+  constexpr int V = 16 / sizeof(TOut);  // entries per 16-byte vector
+  const int64_t t0 = (int64_t)f * grid_h * grid_w + (int64_t)r0 * grid_w;
+  const int PV = P / V;
+  const int nvec = nr * grid_w * PV;
+  auto offset = [&](int e) { return ((int64_t)h * T + t0 + e / PV) * P + (e % PV) * V; };
+  // the source vectors are loaded first, so their latency covers the
+  // evaluation of the t-axis angles (up to kRetimeRegs vectors per thread;
+  // larger rows take the loop below)
+  constexpr int kRetimeRegs = 4;
+  uint4 cv[kRetimeRegs], sv[kRetimeRegs];
+#pragma unroll
+  for (int i = 0; i < kRetimeRegs; ++i) {
+    const int e = threadIdx.x + i * 256;
+    if (e < nvec) {
+      cv[i] = *reinterpret_cast<const uint4*>(cos_src + offset(e));
+      sv[i] = *reinterpret_cast<const uint4*>(sin_src + offset(e));
+    }
+  }
   for (int j = threadIdx.x; j < P; j += blockDim.x) {
     const int g = h * P + j;
     float c = 1.0f, sn = 0.0f;
@@ -224,16 +242,10 @@ __global__ void __launch_bounds__(256) rope_table_retime_kernel(
     tfac[2 * j + 1] = sn;
   }
   __syncthreads();
-  constexpr int V = 16 / sizeof(TOut);  // entries per 16-byte vector
-  const int64_t t0 = (int64_t)f * grid_h * grid_w + (int64_t)r0 * grid_w;
-  const int PV = P / V;
-  for (int e = threadIdx.x; e < nr * grid_w * PV; e += blockDim.x) {
-    const int tl = e / PV, j0 = (e % PV) * V;
-    const int64_t o = ((int64_t)h * T + t0 + tl) * P + j0;
-    uint4 cv = *reinterpret_cast<const uint4*>(cos_src + o);
-    uint4 sv = *reinterpret_cast<const uint4*>(sin_src + o);
-    TOut* ce = reinterpret_cast<TOut*>(&cv);
-    TOut* se = reinterpret_cast<TOut*>(&sv);
+  auto patch_store = [&](int e, uint4 c4, uint4 s4) {
+    const int j0 = (e % PV) * V;
+    TOut* ce = reinterpret_cast<TOut*>(&c4);
+    TOut* se = reinterpret_cast<TOut*>(&s4);
 #pragma unroll
     for (int i = 0; i < V; ++i) {
       const int g = h * P + j0 + i;
@@ -247,9 +259,17 @@ __global__ void __launch_bounds__(256) rope_table_retime_kernel(
         }
       }
     }
-    *reinterpret_cast<uint4*>(cos_out + o) = cv;
-    *reinterpret_cast<uint4*>(sin_out + o) = sv;
+    *reinterpret_cast<uint4*>(cos_out + offset(e)) = c4;
+    *reinterpret_cast<uint4*>(sin_out + offset(e)) = s4;
+  };
+#pragma unroll
+  for (int i = 0; i < kRetimeRegs; ++i) {
+    const int e = threadIdx.x + i * 256;
+    if (e < nvec) patch_store(e, cv[i], sv[i]);
   }
+  for (int e = threadIdx.x + kRetimeRegs * 256; e < nvec; e += 256)
+    patch_store(e, *reinterpret_cast<const uint4*>(cos_src + offset(e)),
+                *reinterpret_cast<const uint4*>(sin_src + offset(e)));
 }
 
 // ---------------------------------------------------------------------------

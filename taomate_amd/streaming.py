@@ -178,9 +178,12 @@ class ChunkStream:
         it at the memory's own positions and swap it into the cache in place."""
         n = self.memory_frames * self.hw
         tail = x_recent[:, -n:]
-        ema = self.memory_state * (1.0 - self.memory_beta) + tail.float() * self.memory_beta
-        if self.memory_tether > 0.0:
-            ema = ema * (1.0 - self.memory_tether) + self.memory_anchor * self.memory_tether
+        # (1 - t) ((1 - b) m + b x) + t a in place, three float32 passes
+        # (the bf16 frames are widened inside the add) instead of seven
+        b, t = self.memory_beta, self.memory_tether if self.memory_tether > 0.0 else 0.0
+        ema = self.memory_state.mul_((1.0 - b) * (1.0 - t)).add_(tail, alpha=b * (1.0 - t))
+        if t > 0.0:
+            ema.add_(self.memory_anchor, alpha=t)
         self.memory_state = ema
         km, vm = self._prefill_segment(self.memory_state.to(x_recent.dtype), self.anchor_frames,
                                        self.memory_frames)

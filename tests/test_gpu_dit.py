@@ -24,7 +24,7 @@ B, GH, GW, NF, F0, NCACHE_F = 2, 4, 6, 3, 6, 6
 LA, LA_CACHE, A0, LT = 10, 40, 60, 16
 
 
-def _inputs():
+def _inputs(CFG=CFG):
     g = torch.Generator().manual_seed(33)
     r = lambda *s: torch.randn(*s, generator=g).to(torch.bfloat16).float()
     hw = GH * GW
@@ -42,7 +42,7 @@ def _inputs():
     return x
 
 
-def _pes(dev=None):
+def _pes(dev=None, CFG=CFG):
     """(video, audio, video cross, audio cross) RoPE tables; oracle when dev is None."""
     vd, cross = CFG.video_dim, CFG.audio_heads * CFG.audio_d_head
     hw = GH * GW
@@ -268,6 +268,35 @@ def test_loaded_checkpoint_matches_oracle(dev, tmp_path):
                                         bf(x["actx"]), bf(x["mask"]), bf(x["mask"]), *_pes(dev), caches)
     torch.cuda.synchronize()
     assert vo.shape == (B, NF * hw, CFG.out_channels)
+    cv, ca = cosine(vo, ref_v), cosine(ao, ref_a)
+    assert cv >= 0.999 and ca >= 0.999, (cv, ca)
+    for out, ref in ((vo, ref_v), (ao, ref_a)):
+        err = (out.float().cpu() - ref).abs().max().item()
+        assert err <= 3e-2 * ref.abs().max().item(), err
+
+
+@pytest.mark.timeout(600)
+def test_48_block_stack_matches_oracle(dev):
+    """All 48 blocks of the model's depth composed, at a reduced width (video
+    8 x 64, audio 4 x 64): one denoising step over dense caches against the
+    fp32 oracle's 48-block forward (the full-width 48-block step is checked
+    for its properties in test_gpu_dit_full.py; its fp32 oracle would need
+    75 GB of weights)."""
+    cfg = D.AVConfig(num_layers=48, video_dim=512, audio_dim=256, video_heads=8, audio_heads=4,
+                     video_d_head=64, audio_d_head=64)
+    model = D.build_model(cfg, dev, seed=13).fuse_qkv_()
+    params = {n: p.detach().float().cpu() for n, p in model.named_parameters()}
+    x = _inputs(cfg)
+    ref_v, ref_a = OD.forward_chunk(params, cfg, x["video"], x["audio"], x["sigma"], x["vctx"], x["actx"],
+                                    x["mask"].float(), x["mask"].float(), *_pes(None, cfg), x["cache"])
+    bf = lambda t: t.to(dev, torch.bfloat16)
+    caches = [T.LayerKVCache(video_self_k=bf(c["video_self_k"]), video_self_v=bf(c["video_self_v"]),
+                             audio_self_k=bf(c["audio_self_k"]), audio_self_v=bf(c["audio_self_v"]))
+              for c in x["cache"]]
+    with torch.no_grad():
+        vo, ao, _ = model.forward_chunk(bf(x["video"]), bf(x["audio"]), x["sigma"].to(dev), bf(x["vctx"]),
+                                        bf(x["actx"]), bf(x["mask"]), bf(x["mask"]), *_pes(dev, cfg), caches)
+    torch.cuda.synchronize()
     cv, ca = cosine(vo, ref_v), cosine(ao, ref_a)
     assert cv >= 0.999 and ca >= 0.999, (cv, ca)
     for out, ref in ((vo, ref_v), (ao, ref_a)):

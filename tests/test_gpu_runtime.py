@@ -109,6 +109,11 @@ def test_two_windows_match_oracle(dev):
         worst = min(worst, cv, ca)
         print(f"block {bi}: cosine video {cv:.6f} audio {ca:.6f}", flush=True)
         assert cv >= 0.999 and ca >= 0.999, (bi, cv, ca)
+        # and elementwise: within 3 % of the block's range (bf16 GEMMs and
+        # attention over three denoise steps and the commit)
+        for out, r in ((v, rv), (a, ra)):
+            err = (out.float() - r).abs().max().item()
+            assert err <= 3e-2 * r.abs().max().item(), (bi, err)
     last = gen.last_cache.layers[1]
     for f in ("video_self_k", "video_self_v", "audio_self_k", "a2v_v", "v2a_k"):
         t = getattr(last, f)

@@ -6,7 +6,10 @@ Follows, op for op:
   _prepare_timestep / cross timestep       ltx_causal/transformer/causal_model.py:426-496
   get_ada_values / get_av_ca_ada_values    ltx_causal/transformer/causal_block.py:434-481
   block_forward_with_cache (sync branch)   ltx_causal/transformer/kv_cache.py:2145-2656
-  text cross-attention without prompt AdaLN  kv_cache.py:1134-1141
+  text cross-attention                     kv_cache.py:1090-1141 (without prompt AdaLN,
+                                           and the LTX-2.3 prompt AdaLN when the
+                                           blocks hold prompt_scale_shift_table;
+                                           prompt timestep kv_cache.py:2876-2895)
   _process_output                          causal_model.py:568-599
   learned-memory adapters (optional)       causal_block.py:108-193, 489-505;
                                            placement kv_cache.py:2217-2330;
@@ -120,10 +123,27 @@ def _apply_steps(x, steps, eps):
     return x
 
 
+def text_cross(p, prefix: str, attn: str, table: str, prompt_table: str, B: int, ts, prompt_ts, x, ctx, mask,
+               heads: int, d_head: int, eps: float):
+    """_apply_text_cross_attention_for_inference (kv_cache.py:1090-1141).
+    Without prompt AdaLN: attention of rms_norm(x) over the context.  With it
+    (the block holds ``prompt_table``): the query input is rms_norm(x) *
+    (1 + scale) + shift from rows 6..8 of the block's table (shift, scale,
+    gate), the context is modulated by (shift, scale) = prompt table + prompt
+    timestep, and the output is scaled by the gate."""
+    w = attn_weights(p, prefix + attn, heads, d_head)
+    if prefix + prompt_table not in p:
+        return OA.text_cross_attention(w, rms_norm(x, eps), ctx, mask)
+    sh_q, sc_q, g = ada_values(p[prefix + table], B, ts, slice(6, 9))
+    kv = p[prefix + prompt_table][None, None] + prompt_ts.reshape(B, prompt_ts.shape[1], 2, -1)
+    sh_kv, sc_kv = kv.unbind(dim=2)
+    return OA.text_cross_attention(w, rms_norm(x, eps) * (1 + sc_q) + sh_q, ctx * (1 + sc_kv) + sh_kv, mask) * g
+
+
 def block_forward(p: Dict[str, torch.Tensor], prefix: str, cfg, vx, ax, v_ts, a_ts, video_pe, audio_pe,
                   video_cross_pe, audio_cross_pe, video_ctx, audio_ctx, video_mask, audio_mask, v_ss, v_gate,
                   a_ss, a_gate, cache: Dict[str, Optional[torch.Tensor]], video_memory=None, audio_memory=None,
-                  color_memory=None):
+                  color_memory=None, v_prompt=None, a_prompt=None):
     """kv_cache.py:2145-2656, synchronous branch.  ``cache`` holds dense
     video_self_k/v, audio_self_k/v, a2v_k/v, v2a_k/v (or None).  Returns
     (vx, ax, new_cache): new_cache holds each field with this chunk's K/V
@@ -142,8 +162,8 @@ def block_forward(p: Dict[str, torch.Tensor], prefix: str, cfg, vx, ax, v_ts, a_
     vx = vx + out * g
     if mode == "memory_kv_side_branch":
         vx = _apply_steps(vx, v_steps, eps)
-    v_text = OA.text_cross_attention(attn_weights(p, prefix + "attn2.", vh, vdh), rms_norm(vx, eps), video_ctx,
-                                     video_mask)
+    v_text = text_cross(p, prefix, "attn2.", "scale_shift_table", "prompt_scale_shift_table", B, v_ts, v_prompt, vx,
+                        video_ctx, video_mask, vh, vdh, eps)
     sh, sc, g = ada_values(t("audio_scale_shift_table"), B, a_ts, slice(0, 3))
     out, as_k, as_v = OA.attention_with_cache(attn_weights(p, prefix + "audio_attn1.", ah, adh),
                                               rms_norm(ax, eps) * (1 + sc) + sh, None, audio_pe, None,
@@ -151,8 +171,8 @@ def block_forward(p: Dict[str, torch.Tensor], prefix: str, cfg, vx, ax, v_ts, a_
     ax = ax + out * g
     if mode == "memory_kv_side_branch":
         ax = _apply_steps(ax, a_steps, eps)
-    a_text = OA.text_cross_attention(attn_weights(p, prefix + "audio_attn2.", ah, adh), rms_norm(ax, eps),
-                                     audio_ctx, audio_mask)
+    a_text = text_cross(p, prefix, "audio_attn2.", "audio_scale_shift_table", "audio_prompt_scale_shift_table", B,
+                        a_ts, a_prompt, ax, audio_ctx, audio_mask, ah, adh, eps)
     vx = vx + v_text
     ax = ax + a_text
     if mode == "cross_attn_adapter":
@@ -227,11 +247,21 @@ def forward_chunk(p: Dict[str, torch.Tensor], cfg, video_latent, audio_latent, s
     aview = lambda x: per_token(x.view(B, -1, x.shape[-1]), ax.shape[1])
     v_ts, v_emb, a_ts, a_emb = vview(v_ts), vview(v_emb), aview(a_ts), aview(a_emb)
     v_ss, a_ss, v_gate, a_gate = vview(v_ss), aview(a_ss), vview(v_gate), aview(a_gate)
+    v_prompt = a_prompt = None
+    if "prompt_adaln_single.linear.weight" in p:
+        # LTX-2.3 prompt timestep (kv_cache.py:2876-2895): one value per sample,
+        # the mean of per-frame / per-token sigmas
+        vs = sigma.mean(dim=-1, keepdim=True) if sigma.dim() == 2 else sigma
+        as_ = sigma if audio_sigma is None else audio_sigma
+        as_ = as_.mean(dim=-1, keepdim=True) if as_.dim() == 2 else as_
+        v_prompt = adaln_single(p, "prompt_adaln_single.", (vs * cfg.timestep_scale_multiplier).flatten())[0]
+        a_prompt = adaln_single(p, "audio_prompt_adaln_single.", (as_ * cfg.timestep_scale_multiplier).flatten())[0]
+        v_prompt, a_prompt = v_prompt.view(B, -1, v_prompt.shape[-1]), a_prompt.view(B, -1, a_prompt.shape[-1])
     new_caches = []
     for i in range(cfg.num_layers):
         vx, ax, nc = block_forward(p, f"transformer_blocks.{i}.", cfg, vx, ax, v_ts, a_ts, video_pe, audio_pe,
                                    video_cross_pe, audio_cross_pe, video_ctx, audio_ctx, video_mask, audio_mask,
-                                   v_ss, v_gate, a_ss, a_gate, caches[i], vm, am, cm)
+                                   v_ss, v_gate, a_ss, a_gate, caches[i], vm, am, cm, v_prompt, a_prompt)
         new_caches.append(nc)
 
     def head(table, proj, x, emb):

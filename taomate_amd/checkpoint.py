@@ -6,9 +6,10 @@ state_dict}`` whose keys are the wrapper's ``model.<parameter>`` names, read
 here with ``torch.load(..., weights_only=True, mmap=True)`` (no code runs
 from the file) or from a ``.safetensors`` file of the same keys.  The block
 configuration is read off the tensors the way the reference auto-detects it
-(layer count, widths, gated attention, learned-memory adapters and FiLM);
-features this build does not run (cross-attention AdaLN tables, audio sink
-tokens, caption projection) are refused by name instead of being dropped.
+(layer count, widths, gated attention, the LTX-2.3 text cross-attention
+AdaLN, learned-memory adapters and FiLM); features this build does not run
+(audio sink tokens, caption projection) are refused by name instead of being
+dropped.
 The model is built on the meta device and takes the checkpoint's tensors
 with ``assign=True`` (no second copy of the weights), then moves to the
 target device.
@@ -58,8 +59,10 @@ def detect_config(sd: Mapping[str, torch.Tensor], *, video_d_head: int = 128, au
         "caption projection": any(k.startswith("caption_projection.") for k in sd),
     }
     vd, in_ch = _shape(sd, "patchify_proj.weight")
-    if _shape(sd, "adaln_single.linear.weight")[0] == 9 * vd:
-        unsupported["cross-attention AdaLN"] = True
+    # LTX-2.3 text cross-attention AdaLN: 9 modulation rows (model_runtime.py:256-261)
+    coeff = _shape(sd, "adaln_single.linear.weight")[0] // vd
+    if coeff not in (6, 9):
+        unsupported[f"an AdaLN of {coeff} coefficients"] = True
     bad = [name for name, hit in unsupported.items() if hit]
     if bad:
         raise NotImplementedError(f"checkpoint uses features this build does not run: {', '.join(bad)}")
@@ -87,7 +90,8 @@ def detect_config(sd: Mapping[str, torch.Tensor], *, video_d_head: int = 128, au
     return AVConfig(num_layers=layers, video_dim=vd, audio_dim=ad, video_heads=v_inner // video_d_head,
                     audio_heads=a_inner // audio_d_head, video_d_head=video_d_head, audio_d_head=audio_d_head,
                     in_channels=in_ch, out_channels=_shape(sd, "proj_out.weight")[0],
-                    apply_gated_attention=any("to_gate_logits" in k for k in sd), **kw)
+                    apply_gated_attention=any("to_gate_logits" in k for k in sd), cross_attention_adaln=coeff == 9,
+                    **kw)
 
 
 def load_generator(model_ckpt_path: str, device="cuda", dtype: torch.dtype = torch.bfloat16,

@@ -131,6 +131,9 @@ class AVConfig:
     timestep_scale_multiplier: float = 1000.0
     av_ca_timestep_scale_multiplier: float = 1.0
     apply_gated_attention: bool = False   # per-head output gates (to_gate_logits)
+    # LTX-2.3 text cross-attention AdaLN (causal_model.py:180-184): 9-row
+    # modulation tables, prompt tables and prompt_adaln_single modules
+    cross_attention_adaln: bool = False
     # learned long-memory adapters (causal_model.py:194-203), off by default
     learned_memory_enabled: bool = False
     learned_memory_mode: str = "cross_attn_adapter"   # or "memory_kv_side_branch"
@@ -217,13 +220,18 @@ class AVBlock(nn.Module):
         self.attn2 = CausalLTXAttention(vd, context_dim=vd, heads=cfg.video_heads, dim_head=cfg.video_d_head,
                                         norm_eps=cfg.norm_eps, apply_gated_attention=gated)
         self.ff = FeedForward(vd, vd)
-        self.scale_shift_table = nn.Parameter(torch.empty(6, vd))
+        coeff = 9 if cfg.cross_attention_adaln else 6   # causal_block.py:248-255
+        self.cross_attention_adaln = bool(cfg.cross_attention_adaln)
+        self.scale_shift_table = nn.Parameter(torch.empty(coeff, vd))
         self.audio_attn1 = CausalLTXAttention(ad, heads=cfg.audio_heads, dim_head=cfg.audio_d_head,
                                               norm_eps=cfg.norm_eps, apply_gated_attention=gated)
         self.audio_attn2 = CausalLTXAttention(ad, context_dim=ad, heads=cfg.audio_heads, dim_head=cfg.audio_d_head,
                                               norm_eps=cfg.norm_eps, apply_gated_attention=gated)
         self.audio_ff = FeedForward(ad, ad)
-        self.audio_scale_shift_table = nn.Parameter(torch.empty(6, ad))
+        self.audio_scale_shift_table = nn.Parameter(torch.empty(coeff, ad))
+        if cfg.cross_attention_adaln:   # causal_block.py:343-348
+            self.prompt_scale_shift_table = nn.Parameter(torch.empty(2, vd))
+            self.audio_prompt_scale_shift_table = nn.Parameter(torch.empty(2, ad))
         self.audio_to_video_attn = CausalLTXAttention(vd, context_dim=ad, heads=cfg.audio_heads,
                                                       dim_head=cfg.audio_d_head, norm_eps=cfg.norm_eps,
                                                       apply_gated_attention=gated)
@@ -319,13 +327,33 @@ def _all_blocks_ada(blocks, batch: int, v_ts, a_ts, v_ss, v_gate, a_ss, a_gate) 
             for i in range(len(blocks))]
 
 
+def _text_cross(block: AVBlock, attn: CausalLTXAttention, x: torch.Tensor, xn: torch.Tensor, ctx: torch.Tensor,
+                mask: Optional[torch.Tensor], ts: torch.Tensor, prompt_ts: Optional[torch.Tensor],
+                table: torch.Tensor, prompt_table: Optional[torch.Tensor], ada_q: Optional[tuple]) -> torch.Tensor:
+    """_apply_text_cross_attention_for_inference (kv_cache.py:1090-1141).
+    ``xn`` is rms_norm(x).  Without prompt AdaLN the query input is xn.  With
+    it (LTX-2.3): (shift, scale, gate) from rows 6..8 of the block's table,
+    the query input rms_norm(x) * (1 + scale) + shift, the context modulated
+    by (shift, scale) = prompt table + prompt timestep, and the output scaled
+    by the gate (the residual adds it ungated, as without AdaLN)."""
+    if prompt_table is None:
+        return attn(xn, context=ctx, mask=mask)   # kv_cache.py:1134-1141
+    B = x.shape[0]
+    sh_q, sc_q, g = ada_q if ada_q is not None else block.get_ada_values(table, B, ts, slice(6, 9))
+    kv = (prompt_table[None, None].to(device=x.device, dtype=x.dtype)
+          + prompt_ts.reshape(B, prompt_ts.shape[1], 2, -1)).unbind(dim=2)
+    ctx_mod = ctx * (1 + kv[1]) + kv[0]
+    return attn(_modulate(x, sc_q, sh_q, block.norm_eps), context=ctx_mod, mask=mask) * g
+
+
 def block_forward_with_cache(block: AVBlock, vx: torch.Tensor, ax: torch.Tensor, v_ts: torch.Tensor,
                              a_ts: torch.Tensor, video_pe, audio_pe, video_cross_pe, audio_cross_pe,
                              video_ctx: torch.Tensor, audio_ctx: torch.Tensor, video_mask: Optional[torch.Tensor],
                              audio_mask: Optional[torch.Tensor], v_cross_ss: torch.Tensor, v_cross_gate: torch.Tensor,
                              a_cross_ss: torch.Tensor, a_cross_gate: torch.Tensor, cache: LayerKVCache,
                              video_memory: Optional[torch.Tensor] = None, audio_memory: Optional[torch.Tensor] = None,
-                             color_memory: Optional[torch.Tensor] = None, ada: Optional[Dict[str, tuple]] = None):
+                             color_memory: Optional[torch.Tensor] = None, ada: Optional[Dict[str, tuple]] = None,
+                             v_prompt: Optional[torch.Tensor] = None, a_prompt: Optional[torch.Tensor] = None):
     """kv_cache.py:2145-2656 (synchronous branch): video self -> video text ->
     audio self -> audio text -> A2V -> V2A -> video FFN -> audio FFN.
     Returns (vx, ax, cache with the chunk's K/V appended).
@@ -357,7 +385,9 @@ def block_forward_with_cache(block: AVBlock, vx: torch.Tensor, ax: torch.Tensor,
     vx, vn = _residual(vx, out, g, norm=True, eps=eps)
     if side:
         vx, vn = _apply_memory(vx, vn, v_steps, eps, need_norm=True)
-    v_text = block.attn2(vn, context=video_ctx, mask=video_mask)   # kv_cache.py:1134-1141
+    v_text = _text_cross(block, block.attn2, vx, vn, video_ctx, video_mask, v_ts, v_prompt,
+                         block.scale_shift_table, getattr(block, "prompt_scale_shift_table", None),
+                         ada["v"][6:9] if ada and block.cross_attention_adaln else None)
     # audio self-attention and text cross-attention
     sh, sc, g = ada["a"][0:3] if ada else block.get_ada_values(block.audio_scale_shift_table, B, a_ts, slice(0, 3))
     out, as_k, as_v = attention_with_cache(block.audio_attn1, _modulate(ax, sc, sh, eps), None, audio_pe, None,
@@ -365,7 +395,9 @@ def block_forward_with_cache(block: AVBlock, vx: torch.Tensor, ax: torch.Tensor,
     ax, an = _residual(ax, out, g, norm=True, eps=eps)
     if side:
         ax, an = _apply_memory(ax, an, a_steps, eps, need_norm=True)
-    a_text = block.audio_attn2(an, context=audio_ctx, mask=audio_mask)
+    a_text = _text_cross(block, block.audio_attn2, ax, an, audio_ctx, audio_mask, a_ts, a_prompt,
+                         block.audio_scale_shift_table, getattr(block, "audio_prompt_scale_shift_table", None),
+                         ada["a"][6:9] if ada and block.cross_attention_adaln else None)
     vx, vn = _residual(vx, v_text, norm=after_text and v_mem, eps=eps)
     ax, an = _residual(ax, a_text, norm=after_text and a_mem, eps=eps)
     if after_text:
@@ -407,8 +439,11 @@ class AVModel(nn.Module):
         vd, ad = cfg.video_dim, cfg.audio_dim
         self.patchify_proj = nn.Linear(cfg.in_channels, vd)
         self.audio_patchify_proj = nn.Linear(cfg.in_channels, ad)
-        self.adaln_single = AdaLayerNormSingle(vd, 6)
-        self.audio_adaln_single = AdaLayerNormSingle(ad, 6)
+        coeff = 9 if cfg.cross_attention_adaln else 6   # causal_model.py:246-283
+        self.adaln_single = AdaLayerNormSingle(vd, coeff)
+        self.audio_adaln_single = AdaLayerNormSingle(ad, coeff)
+        self.prompt_adaln_single = AdaLayerNormSingle(vd, 2) if cfg.cross_attention_adaln else None
+        self.audio_prompt_adaln_single = AdaLayerNormSingle(ad, 2) if cfg.cross_attention_adaln else None
         self.av_ca_video_scale_shift_adaln_single = AdaLayerNormSingle(vd, 4)
         self.av_ca_audio_scale_shift_adaln_single = AdaLayerNormSingle(ad, 4)
         self.av_ca_a2v_gate_adaln_single = AdaLayerNormSingle(vd, 1)
@@ -534,12 +569,21 @@ class AVModel(nn.Module):
                                             self.av_ca_v2a_gate_adaln_single, B, dt)
         v_ts, v_emb, v_ss, v_gate = (self._per_token(t, Lv) for t in (v_ts, v_emb, v_ss, v_gate))
         a_ts, a_emb, a_ss, a_gate = (self._per_token(t, La) for t in (a_ts, a_emb, a_ss, a_gate))
+        v_prompt = a_prompt = None
+        if self.cfg.cross_attention_adaln:
+            # LTX-2.3 prompt timestep (kv_cache.py:2876-2895): one value per
+            # sample, the mean of per-frame / per-token sigmas
+            vs = sigma.mean(dim=-1, keepdim=True) if sigma.dim() == 2 else sigma
+            as_ = audio_sigma.mean(dim=-1, keepdim=True) if audio_sigma.dim() == 2 else audio_sigma
+            v_prompt, _ = self._timestep(vs, self.prompt_adaln_single, B, dt)
+            a_prompt, _ = self._timestep(as_, self.audio_prompt_adaln_single, B, dt)
         new_caches = []
         ada = _all_blocks_ada(self.transformer_blocks, B, v_ts, a_ts, v_ss, v_gate, a_ss, a_gate)
         for blk, cache, blk_ada in zip(self.transformer_blocks, caches, ada):
             vx, ax, nc = block_forward_with_cache(blk, vx, ax, v_ts, a_ts, video_pe, audio_pe, video_cross_pe,
                                                   audio_cross_pe, video_ctx, audio_ctx, video_mask, audio_mask,
-                                                  v_ss, v_gate, a_ss, a_gate, cache, vm, am, cm, ada=blk_ada)
+                                                  v_ss, v_gate, a_ss, a_gate, cache, vm, am, cm, ada=blk_ada,
+                                                  v_prompt=v_prompt, a_prompt=a_prompt)
             new_caches.append(nc if commit else cache)
             del nc
         if kv_cache_only:

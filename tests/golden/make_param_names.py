@@ -19,14 +19,15 @@ a parameter, and the torch leaves register what torch registers
 "0", "1", ...).  Classes that are not ``nn.Module`` subclasses (the mask
 builder) hold no parameters.
 
-Two configurations are written, both with what load_model_generator detects
-for the 22B V2 checkpoint and what taomate/inference/model.py:20-49 passes
-(no audio sink tokens, caption projection in the text connector, no
-cross-attention AdaLN):
-  * "base": CausalLTXModelConfig's defaults otherwise (48 blocks, 4096 / 2048);
+Three configurations are written, all with what load_model_generator
+detects for the 22B V2 checkpoint and what taomate/inference/model.py:20-49
+passes (no audio sink tokens, caption projection in the text connector):
+  * "base": CausalLTXModelConfig's defaults otherwise (48 blocks, 4096 / 2048,
+    no cross-attention AdaLN);
   * "production": plus gated attention, learned memory (kv side branch,
     every 4th block, 512 / 256, 8 heads) and the colour FiLM (hidden 256,
-    condition 4 x 128).
+    condition 4 x 128);
+  * "ltx23": "production" with the LTX-2.3 text cross-attention AdaLN.
 Per configuration the fixture holds the top-level parameters and the
 per-block parameters of a block without and with the memory adapters, and
 which blocks have them, so the full name set is top-level plus
@@ -58,6 +59,14 @@ CONFIGS = {
                        learned_memory_video_dim=512, learned_memory_audio_dim=256, learned_memory_heads=8,
                        learned_memory_color_film_enabled=True, learned_memory_color_condition_dim=4 * 128,
                        learned_memory_color_film_hidden_dim=256),
+    # the LTX-2.3 base (ltx-2.3-22b-dev, README.md:72-123): text cross-attention
+    # AdaLN, which load_model_generator detects from 9-row modulation tables
+    "ltx23": dict(num_audio_sink_tokens=0, caption_proj_before_connector=True, cross_attention_adaln=True,
+                  apply_gated_attention=True, learned_memory_enabled=True,
+                  learned_memory_mode="memory_kv_side_branch", learned_memory_layer_interval=4,
+                  learned_memory_video_dim=512, learned_memory_audio_dim=256, learned_memory_heads=8,
+                  learned_memory_color_film_enabled=True, learned_memory_color_condition_dim=4 * 128,
+                  learned_memory_color_film_hidden_dim=256),
 }
 
 

@@ -46,7 +46,8 @@ def _product(cfg):
     return m, {k: tuple(v.shape) for k, v in m.state_dict().items()}
 
 
-@pytest.mark.parametrize("name,extra", [("base", {}), ("production", PRODUCTION)])
+@pytest.mark.parametrize("name,extra", [("base", {}), ("production", PRODUCTION),
+                                        ("ltx23", dict(PRODUCTION, cross_attention_adaln=True))])
 def test_parameter_names_and_shapes_match_reference(name, extra):
     ref = _reference(name)
     _, got = _product(D.AVConfig(**extra))
@@ -55,15 +56,18 @@ def test_parameter_names_and_shapes_match_reference(name, extra):
     assert not bad, [(k, got[k], ref[k]) for k in bad[:5]]
 
 
-def test_detect_config_reads_reference_shapes():
+@pytest.mark.parametrize("name,adaln", [("production", False), ("ltx23", True)])
+def test_detect_config_reads_reference_shapes(name, adaln):
     """A state dict with the reference's production names and shapes (meta
-    tensors) detects to the production configuration and loads strictly."""
-    ref = _reference("production")
+    tensors) detects to the production configuration and loads strictly; the
+    LTX-2.3 layout (9-row modulation tables, prompt tables) detects with the
+    text cross-attention AdaLN."""
+    ref = _reference(name)
     sd = {k: torch.empty(v, device="meta") for k, v in ref.items()}
     cfg = C.detect_config(sd, learned_memory_mode="memory_kv_side_branch")
-    want = D.AVConfig(**PRODUCTION)
+    want = D.AVConfig(**PRODUCTION, cross_attention_adaln=adaln)
     for f in ("num_layers", "video_dim", "audio_dim", "video_heads", "audio_heads", "video_d_head", "audio_d_head",
-              "in_channels", "out_channels") + tuple(PRODUCTION):
+              "in_channels", "out_channels", "cross_attention_adaln") + tuple(PRODUCTION):
         assert getattr(cfg, f) == getattr(want, f), f
     m, _ = _product(cfg)
     missing, unexpected = m.load_state_dict(sd, strict=False, assign=True)

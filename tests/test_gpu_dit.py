@@ -302,3 +302,36 @@ def test_48_block_stack_matches_oracle(dev):
     for out, ref in ((vo, ref_v), (ao, ref_a)):
         err = (out.float().cpu() - ref).abs().max().item()
         assert err <= 3e-2 * ref.abs().max().item(), err
+
+
+@pytest.mark.parametrize("per_frame", [False, True], ids=["per_sample_sigma", "per_frame_sigma"])
+def test_ltx23_text_adaln_matches_oracle(dev, per_frame):
+    """The LTX-2.3 text cross-attention AdaLN (9-row modulation tables, prompt
+    tables, prompt_adaln_single modules; kv_cache.py:1090-1141, prompt
+    timestep :2876-2895) through the 2-block stack against the oracle, with a
+    sigma per sample and per latent frame (the prompt timestep then takes
+    the frames' mean), both streams' text keys 25 % padded."""
+    cfg = D.AVConfig(num_layers=2, video_dim=512, audio_dim=256, video_heads=8, audio_heads=4, video_d_head=64,
+                     audio_d_head=64, cross_attention_adaln=True, apply_gated_attention=True)
+    model = D.build_model(cfg, dev, seed=17)
+    assert model.transformer_blocks[0].scale_shift_table.shape == (9, 512)
+    params = {n: p.detach().float().cpu() for n, p in model.named_parameters()}
+    x = _inputs(cfg)
+    g = torch.Generator().manual_seed(19)
+    sigma = torch.rand(B, NF, generator=g) if per_frame else x["sigma"]
+    a_sigma = torch.rand(B, generator=g) if per_frame else None
+    ref_v, ref_a = OD.forward_chunk(params, cfg, x["video"], x["audio"], sigma, x["vctx"], x["actx"],
+                                    x["mask"].float(), x["mask"].float(), *_pes(None, cfg), x["cache"],
+                                    audio_sigma=a_sigma)
+    caches = _arena_caches(dev, cfg, x["cache"])
+    bf = lambda t: t.to(dev, torch.bfloat16)
+    with torch.no_grad():
+        vo, ao, _ = model.forward_chunk(bf(x["video"]), bf(x["audio"]), sigma.to(dev), bf(x["vctx"]),
+                                        bf(x["actx"]), bf(x["mask"]), bf(x["mask"]), *_pes(dev, cfg), caches,
+                                        audio_sigma=None if a_sigma is None else a_sigma.to(dev))
+    torch.cuda.synchronize()
+    cv, ca = cosine(vo, ref_v), cosine(ao, ref_a)
+    assert cv >= 0.999 and ca >= 0.999, (cv, ca)
+    for out, ref in ((vo, ref_v), (ao, ref_a)):
+        err = (out.float().cpu() - ref).abs().max().item()
+        assert err <= 3e-2 * ref.abs().max().item(), err

@@ -197,7 +197,7 @@ def _ffn_path(p, x, eps=1e-6):
     for s, tab, ts, ff in (("vx", "scale_shift_table", "v_ts", "ff."), ("ax", "audio_scale_shift_table", "a_ts",
                                                                          "audio_ff.")):
         d = x[s].shape[-1]
-        t = p[tab][None, None] + x[ts].reshape(B, 1, 6, d)
+        t = p[tab][None, None] + x[ts].reshape(B, 1, p[tab].shape[0], d)
         sh, sc, g = t[:, :, 3], t[:, :, 4], t[:, :, 5]
         out.append(x[s] + OD.feed_forward(p, ff, OD.rms_norm(x[s], eps) * (1 + sc) + sh) * g)
     return out
@@ -222,21 +222,23 @@ def _one_key(p, name, ctx):
     return F.linear(v, p[name + "to_out.0.weight"], p[name + "to_out.0.bias"])
 
 
-def _one_token_block(p, x, eps=1e-6, v2a_after_a2v=False):
+def _one_token_block(p, x, eps=1e-6, v2a_after_a2v=False, text=None):
     """The block for one video and one audio token written from the
     reference's order (kv_cache.py:2194-2633) with every attention over one
     key.  ``v2a_after_a2v`` plants a mistake: V2A reading the video norm taken
-    after the A2V residual."""
+    after the A2V residual.  ``text``: the two text terms, when not the plain
+    to_out(to_v(context)) (the prompt-AdaLN ones)."""
     B = x["vx"].shape[0]
     vd, ad = x["vx"].shape[-1], x["ax"].shape[-1]
     rms = lambda t: OD.rms_norm(t, eps)
-    vt = p["scale_shift_table"][None, None] + x["v_ts"].reshape(B, 1, 6, vd)
-    at = p["audio_scale_shift_table"][None, None] + x["a_ts"].reshape(B, 1, 6, ad)
+    nv, na = p["scale_shift_table"].shape[0], p["audio_scale_shift_table"].shape[0]
+    vt = p["scale_shift_table"][None, None] + x["v_ts"].reshape(B, 1, nv, vd)
+    at = p["audio_scale_shift_table"][None, None] + x["a_ts"].reshape(B, 1, na, ad)
     vx, ax = x["vx"], x["ax"]
     vx = vx + _one_key(p, "attn1.", rms(vx) * (1 + vt[:, :, 1]) + vt[:, :, 0]) * vt[:, :, 2]
-    v_text = _one_key(p, "attn2.", x["vctx"])
+    v_text = _one_key(p, "attn2.", x["vctx"]) if text is None else text[0]
     ax = ax + _one_key(p, "audio_attn1.", rms(ax) * (1 + at[:, :, 1]) + at[:, :, 0]) * at[:, :, 2]
-    a_text = _one_key(p, "audio_attn2.", x["actx"])
+    a_text = _one_key(p, "audio_attn2.", x["actx"]) if text is None else text[1]
     vx, ax = vx + v_text, ax + a_text
     vca = p["scale_shift_table_a2v_ca_video"][None, None] + torch.cat(
         [x["v_ss"].reshape(B, 1, 4, vd), x["v_gate"].reshape(B, 1, 1, vd)], 2)
@@ -301,3 +303,68 @@ def test_memory_ema_rule_special_cases():
     torch.testing.assert_close(got, want)
     slip = 0.85 * (0.8 * prev + 0.2 * anchor) + 0.15 * cur
     assert (got - slip).abs().max().item() > 1e-3
+
+
+def _adaln_text_case(g, vd=16, ad=8, B=2):
+    """One block with the LTX-2.3 prompt AdaLN: 9-row tables, prompt tables,
+    prompt timesteps; one video and one audio token, one text key each."""
+    p = _block_params(vd, ad, g)
+    r = lambda *s: torch.randn(*s, generator=g) * 0.3
+    p["scale_shift_table"], p["audio_scale_shift_table"] = r(9, vd), r(9, ad)
+    p["prompt_scale_shift_table"], p["audio_prompt_scale_shift_table"] = r(2, vd), r(2, ad)
+    x = _inputs(B, 1, 1, vd, ad, g, Lctx=1)
+    x["v_ts"], x["a_ts"] = r(B, 1, 9 * vd), r(B, 1, 9 * ad)
+    x["v_prompt"], x["a_prompt"] = r(B, 1, 2 * vd), r(B, 1, 2 * ad)
+    return p, x
+
+
+def _adaln_text_closed_form(p, x, stream="v", slip=None):
+    """The text cross-attention term of one stream over a single text key
+    (kv_cache.py:1090-1141): softmax weight 1, so the output is
+    to_out(to_v(ctx * (1 + scale_kv) + shift_kv)) * gate, (shift_kv, scale_kv)
+    = prompt table + prompt timestep in that order, gate = row 8 of the block's
+    table + its timestep slice.  ``slip``: "kv_order" swaps shift and scale,
+    "no_gate" drops the gate, "rows_3_5" takes the gate from row 5."""
+    B = x["vx"].shape[0]
+    tab, ptab, ts, pts, ctx, attn = (("scale_shift_table", "prompt_scale_shift_table", "v_ts", "v_prompt", "vctx",
+                                      "attn2.") if stream == "v" else
+                                     ("audio_scale_shift_table", "audio_prompt_scale_shift_table", "a_ts",
+                                      "a_prompt", "actx", "audio_attn2."))
+    d = x[ctx].shape[-1]
+    kv = p[ptab][None, None] + x[pts].reshape(B, 1, 2, d)
+    sh, sc = kv[:, :, 0], kv[:, :, 1]
+    if slip == "kv_order":
+        sh, sc = sc, sh
+    t9 = p[tab][None, None] + x[ts].reshape(B, 1, 9, d)
+    gate = t9[:, :, 5] if slip == "rows_3_5" else t9[:, :, 8]
+    out = _one_key(p, attn, x[ctx] * (1 + sc) + sh)
+    return out if slip == "no_gate" else out * gate
+
+
+def test_adaln_text_cross_over_one_key():
+    """With the LTX-2.3 prompt AdaLN the text term of each stream is the closed
+    form above; the planted slips (shift / scale of the context swapped, the
+    gate dropped, the gate taken from the feed-forward rows) all differ."""
+    g = torch.Generator().manual_seed(9)
+    p, x = _adaln_text_case(g)
+    B, vd, ad = 2, 16, 8
+    for stream in ("v", "a"):
+        d = vd if stream == "v" else ad
+        xs = x["vx"] if stream == "v" else x["ax"]
+        got = OD.text_cross(p, "", "attn2." if stream == "v" else "audio_attn2.",
+                            "scale_shift_table" if stream == "v" else "audio_scale_shift_table",
+                            "prompt_scale_shift_table" if stream == "v" else "audio_prompt_scale_shift_table", B,
+                            x["v_ts"] if stream == "v" else x["a_ts"], x["v_prompt"] if stream == "v" else x["a_prompt"],
+                            xs, x["vctx"] if stream == "v" else x["actx"], None, 2, d // 2, 1e-6)
+        want = _adaln_text_closed_form(p, x, stream)
+        torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
+        for slip in ("kv_order", "no_gate", "rows_3_5"):
+            assert (got - _adaln_text_closed_form(p, x, stream, slip)).abs().max().item() > 1e-3, (stream, slip)
+    # and inside the block: the one-token block with the text terms replaced by these
+    vx, ax, _ = OD.block_forward(p, "", _cfg(vd, ad), x["vx"], x["ax"], x["v_ts"], x["a_ts"], None, None, None,
+                                 None, x["vctx"], x["actx"], None, None, x["v_ss"], x["v_gate"], x["a_ss"],
+                                 x["a_gate"], {}, v_prompt=x["v_prompt"], a_prompt=x["a_prompt"])
+    text = (_adaln_text_closed_form(p, x, "v"), _adaln_text_closed_form(p, x, "a"))
+    wv, wa = _one_token_block(p, x, text=text)
+    torch.testing.assert_close(vx, wv, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(ax, wa, rtol=1e-5, atol=1e-5)

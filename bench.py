@@ -428,6 +428,56 @@ def cpu_baseline(seconds_budget: float = 20.0):
                       f"torch {torch.__version__}, {platform.processor() or platform.machine()}"}
 
 
+def cold_rates(w, copies: int = 6) -> dict:
+    """The step's HBM kernels with their inputs rotated over ``copies`` sets of
+    q/k/v projection outputs (6 x 56.6 MB, more than the 256 MB last-level
+    cache), so every call reads its inputs from HBM: the rates of the
+    standalone loops (one input set, back to back) are flattered by that
+    cache."""
+    from taomate_amd import kernels
+
+    a = w["arena"]
+    slot = w["slot"]
+    kd, vd = a.slots("k", slot, LQ), a.slots("v", slot, LQ)
+    ks, vs = a.scale_slots("k", slot, LQ), a.scale_slots("v", slot, LQ)
+    sets = [(w["q_lin"].clone(), w["k_lin"].clone(), w["v_lin"].clone()) for _ in range(copies)]
+    kbf = torch.empty(B, LQ, H, D, device=a.device, dtype=torch.bfloat16) if a.fp8 else kd
+    it = {"i": 0}
+
+    def nxt():
+        it["i"] = (it["i"] + 1) % copies
+        return sets[it["i"]]
+
+    def norm():
+        ql, kl, _ = nxt()
+        kernels.qk_rmsnorm_rope(ql, w["q"], w["gq"], 1e-6, w["pe"], H, D, kl, kbf, w["gk"], 1e-6, w["pe"])
+
+    def append():
+        _, kl, vl = nxt()
+        if a.fp8:
+            kernels.kv_append_fp8_pair(kl.view(B, LQ, H, D), kd, ks, vl.view(B, LQ, H, D), vd, vs, FRAME)
+        else:
+            kernels.kv_append(vl.view(B, LQ, H, D), vd)
+
+    def prep():
+        ql, kl, vl = nxt()
+        if a.fp8:
+            kernels.qk_rmsnorm_rope(ql, w["q"], w["gq"], 1e-6, w["pe"], H, D, kl, kbf, w["gk"], 1e-6, w["pe"])
+            kernels.kv_append_fp8_pair(kbf, kd, ks, vl.view(B, LQ, H, D), vd, vs, FRAME)
+        else:
+            kernels.qk_rmsnorm_rope(ql, w["q"], w["gq"], 1e-6, w["pe"], H, D, kl, kbf, w["gk"], 1e-6, w["pe"],
+                                    v_in=vl.view(B, LQ, H, D), v_out=vd)
+
+    for f in (norm, append, prep):
+        for _ in range(copies):
+            f()
+    out = {"norm_ms": time_region(norm, 60), "append_ms": time_region(append, 60), "prep_ms": time_region(prep, 60),
+           "copies": copies, "what": f"inputs rotated over {copies} copies of the q/k/v projection outputs "
+                                     f"({copies * 3 * B * LQ * HD * 2 / 1e6:.0f} MB, beyond the last-level cache)"}
+    del sets
+    return out
+
+
 def measure_steps(step, attn, norm, append, prep, steps: int, warmup: int, settle_seconds: float) -> dict:
     """The C2 step timings for one workload: settle, warm-up, the K timed steps
     (events only at the two ends of the region), an instrumented pass of K
@@ -514,6 +564,7 @@ def fp8_step_bench(dev, steps: int, warmup: int, settle_seconds: float) -> dict:
     w = build_workload(dev, "fp8")
     step, attn, norm, append, prep = make_step(w)
     m = measure_steps(step, attn, norm, append, prep, steps, warmup, settle_seconds)
+    cold = cold_rates(w)
     del step, attn, norm, append, prep, w
     fl = attn_flops()
     ach = fl / (m["ms_attn"] * 1e-3) / 1e12
@@ -534,6 +585,10 @@ def fp8_step_bench(dev, steps: int, warmup: int, settle_seconds: float) -> dict:
                       "GB/s": prep_bytes / (m["ms_prep"] * 1e-3) / 1e9,
                       "frac_hbm": prep_bytes / (m["ms_prep"] * 1e-3) / 1e9 / PEAK_HBM_GBPS,
                       "what": "q/k norm + RoPE, then the fp8 pair append (in the step)"},
+        "hbm_cold": {**cold,
+                     "norm_rope_frac_hbm": norm_rope_bytes() / (cold["norm_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+                     "quantise_frac_hbm": append_bytes("fp8") / (cold["append_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+                     "prep_frac_hbm": prep_bytes / (cold["prep_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBPS},
         "per_step_ms_median": {"step": statistics.median(m["step_ms"]),
                                "attention": statistics.median(m["attn_ms"]),
                                "prep": statistics.median(m["prep_ms"])},
@@ -619,6 +674,7 @@ def main():
         print(json.dumps({"attn_only_ms": ms, "queries": args.attn_queries, "tflops": flops / ms / 1e9}))
         return
     m = measure_steps(step, attn, norm, append, prep, args.steps, args.warmup, args.settle_seconds)
+    cold = cold_rates(w)
     del step, attn, norm, append, prep, w
     ms_step, ms_attn, ms_attn_b2b, ms_prep = m["ms_step"], m["ms_attn"], m["ms_attn_b2b"], m["ms_prep"]
     ms_norm, ms_app, ms_prep_alone, ms_prep_two = m["ms_norm"], m["ms_app"], m["ms_prep_alone"], m["ms_prep_two"]
@@ -668,6 +724,11 @@ def main():
                       "frac_hbm": append_bytes(args.kv) / (ms_app * 1e-3) / 1e9 / PEAK_HBM_GBPS,
                       "what": "V transposed into the key-major arena" if args.kv == "bf16"
                       else "K and V quantised to e4m3 into the arena (one launch)"},
+        "hbm_cold": {**cold,
+                     "norm_rope_frac_hbm": norm_rope_bytes() / (cold["norm_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+                     "append_frac_hbm": append_bytes(args.kv) / (cold["append_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+                     "prep_frac_hbm": (norm_rope_bytes() + append_bytes(args.kv)) / (cold["prep_ms"] * 1e-3) / 1e9
+                     / PEAK_HBM_GBPS},
         "step_prep": {"ms": ms_prep,
                       "GB/s": (norm_rope_bytes() + append_bytes(args.kv)) / (ms_prep * 1e-3) / 1e9,
                       "alone_ms": ms_prep_alone, "two_launches_ms": ms_prep_two,

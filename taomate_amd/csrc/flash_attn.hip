@@ -1116,7 +1116,7 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
   constexpr int PREF = 3;
   // fp8 staging inside the slot program: one unit (a K row chunk, a V half,
   // a load) every kStageStride slots from kStageSlot0 on
-  constexpr int kStageSlot0 = 1, kStageStride = 2;
+  constexpr int kStageSlot0 = 0, kStageStride = 1;
   const uint16_t* vf0 = &vbuf[0][li * VS + hg * 8];
   const uint16_t* kf0 = &kbuf[0][li * KS + hg * 8];
   auto tile = [&](int vb, int kbf, const f32x16_t (&scur)[2], f32x16_t (&snext)[2], const uint32_t (&pprev)[16],

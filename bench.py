@@ -621,6 +621,9 @@ def main():
                     help="run only a plain 256 MiB device copy (scale reference for HBM byte counters)")
     ap.add_argument("--copy-bandwidth", action="store_true",
                     help="time plain device copies of 64 MiB - 4 GiB (the practical HBM ceiling of a streaming kernel)")
+    ap.add_argument("--gemm-ceiling", action="store_true",
+                    help="time hipBLASLt bf16 GEMMs of 4096^3 - 16384^3 (the sustained matrix-core rate of a "
+                         "vendor kernel on this part)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs the hot path on one GPU; --gpus must be 1 "
@@ -653,6 +656,24 @@ def main():
             print(json.dumps({"copy_MiB": mib, "ms": round(ms, 4),
                               "TB/s (read + write)": round(2 * n * 4 / (ms * 1e-3) / 1e12, 3)}))
             del x, y
+        return
+    if args.gemm_ceiling:
+        for n in (4096, 8192, 16384):
+            a = torch.randn(n, n, device=dev, dtype=torch.bfloat16)
+            bm = torch.randn(n, n, device=dev, dtype=torch.bfloat16)
+            c = torch.empty(n, n, device=dev, dtype=torch.bfloat16)
+            gemm = lambda: torch.matmul(a, bm, out=c)  # noqa: E731
+            t0 = time.perf_counter()
+            while time.perf_counter() - t0 < 1.0:  # leave the idle clock state
+                for _ in range(4):
+                    gemm()
+                torch.cuda.synchronize()
+            reps = max(10, int(2e14 / (2 * n ** 3)))
+            ms = time_region(gemm, reps)
+            tf = 2 * n ** 3 / (ms * 1e-3) / 1e12
+            print(json.dumps({"gemm_bf16": f"{n}x{n}x{n}", "ms": round(ms, 4), "TFLOP/s": round(tf, 1),
+                              "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 3), "reps": reps}))
+            del a, bm, c
         return
     w = build_workload(dev, args.kv)
     if not 1 <= args.attn_queries <= LQ:

@@ -1427,9 +1427,11 @@ Slots resident_slots(int threads = 256) {
 // slot (twice as many, half as long) leave their second half to start only
 // when the younger workgroups end, with a CU half busy until they drain
 // (193.7 against 184.8 us for the bf16 step at 1152 x 4608, 8 against 4
-// pieces per tail q-tile).  The fp8 kernel is the other way round (194-196
-// against 200-202 us), so its pieces fill every slot, as do the staged
-// kernel's.  Only worth it when there is at least one whole round
+// pieces per tail q-tile).  The fp8 kernel measured the other way round
+// (194-196 against 200-202 us) while its per-tile barrier also waited for
+// the register-staged loads; without that wait it gains from one piece per
+// CU too (187.6 against 180.4 us).  The staged kernel's pieces fill every
+// slot.  Only worth it when there is at least one whole round
 // (otherwise the grid is a single partial round and the extra combine
 // launch costs more than it saves) and each piece keeps >= 4 key tiles.
 // Zero tail tiles: no split.
@@ -1470,9 +1472,9 @@ inline Slots flash_slots(int64_t D, bool vkey, bool fp8, bool mask, bool pair) {
         : fp8        ? resident_slots<flash_fwd_pipe_kernel<64, true>>()
         : mask       ? resident_slots<flash_fwd_kernel<64, false, true>>()
                      : resident_slots<flash_fwd_kernel<64, false, false>>();
-  // pieces: one per CU for the bf16 pipelined kernel (and the pair kernel,
-  // one workgroup per CU), one per slot for the others (plan_split)
-  if (!vkey) s.pieces = s.slots;
+  // pieces: one per CU for the pipelined kernels (and the pair kernel, one
+  // workgroup per CU), one per slot for the staged kernel (plan_split)
+  if (!vkey && !fp8) s.pieces = s.slots;
   return s;
 }
 

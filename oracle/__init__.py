@@ -25,6 +25,18 @@ How each part is pinned (beyond re-typing the reference):
   checked against brute force over token-id tensors.
 * ``fp8``: all 256 e4m3fn codes round-trip; rounding of midpoints is to even;
   saturation at 448.
+* ``dit``: sinusoid and tanh-GELU closed forms; one-hot modulation tables land
+  every value in its slot; with zeroed attention outputs, and with one video
+  and one audio token, the dual-stream block has closed forms that fix the
+  order of its residuals.
+* ``runtime``: the 3-step denoise with zeroed output heads is a closed form in
+  the noise tape and the sigmas; renorm, colour correction, commit, memory
+  update and retention are checked in their order, each check also run on a
+  mutant carrying a plausible slip; the refresh's block selection and global
+  positions are known answers over five layouts.
+* ``memory``, ``stream``: pooling, resampling, gate and EMA + tether steps from
+  their definitions and special cases; the stream replay is composed only of
+  the functions above.
 
 The reference's Python itself was not imported: every function above is pinned
 by these checks, so no golden vectors had to be generated from it.

@@ -806,17 +806,26 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
   constexpr int BM = kBM, BN = kBN;
   constexpr int NKC = D / 8;
   constexpr int KS = D + 8;
-  constexpr int VS = BN + 8;
+  // V^T tile rows (one head-dim channel, BN keys = 8 chunks of 16 bytes):
+  // with D = 128 two rows share one pad chunk (17 chunks per pair, 17 load
+  // instructions per tile), else each row has its own (9 chunks).  Either
+  // way 16 consecutive rows' same chunk covers 16 distinct 16-byte bank
+  // groups, so a fragment read is conflict-free.
+  constexpr bool VPAIR = (D / 2) * 17 % 64 == 0;
+  constexpr int VS = BN + 8;                      // row stride without pairing
+  constexpr int VPS = 2 * BN + 8;                 // pair stride with pairing
   constexpr int KBUF = BN * KS;
-  constexpr int VBUF = D * VS;
+  constexpr int VBUF = VPAIR ? (D / 2) * VPS : D * VS;
   constexpr int KINS = BN * (NKC + 1) / 64;
-  constexpr int VINS = D * 9 / 64;
+  constexpr int VINS = VPAIR ? (D / 2) * 17 / 64 : D * 9 / 64;
   constexpr int KSLOT = (KINS + 3) / 4;
   constexpr int VSLOT = (VINS + 3) / 4;
   constexpr int DB = D / 32;
   constexpr int QS = D / 16;
   constexpr float kOver = 65536.0f;  // largest per-lane tile sum kept without raising m
-  static_assert(BN * (NKC + 1) % 64 == 0 && D * 9 % 64 == 0, "tile does not split into whole instructions");
+  static_assert(BN * (NKC + 1) % 64 == 0 && (VPAIR || D * 9 % 64 == 0), "tile does not split into whole instructions");
+  // element offset of V^T row r in a V buffer
+  auto vrow = [](int r) { return VPAIR ? (r >> 1) * VPS + (r & 1) * BN : r * VS; };
 
   __shared__ __attribute__((aligned(16))) uint16_t kbuf[2][KBUF];
   __shared__ __attribute__((aligned(16))) uint16_t vbuf[2][VBUF];
@@ -851,12 +860,20 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
     c = pch % (NKC + 1);
     c = c < NKC ? c : 0;
   };
+  // the (channel, 16-byte chunk) load slot i of this lane fills; a pad slot
+  // re-reads a valid chunk
   auto vpos = [&](int i, int& d, int& c) {
     const int pch = (wave + 4 * i) * 64 + lane;
-    d = pch / 9;
-    d = d < D ? d : 0;
-    c = pch % 9;
-    c = c < 8 ? c : 0;
+    if constexpr (VPAIR) {
+      const int q = pch % 17;
+      d = 2 * (pch / 17) + (q < 16 ? q >> 3 : 0);
+      c = q < 16 ? (q & 7) : 0;
+    } else {
+      d = pch / 9;
+      d = d < D ? d : 0;
+      c = pch % 9;
+      c = c < 8 ? c : 0;
+    }
   };
   int koff[KSLOT], voff[VSLOT];
 #pragma unroll
@@ -981,11 +998,12 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
     // channels 4*half + {0, 1} and {2, 3} of keys (0, 1) and (2, 3)
     const uint32_t k01a = __builtin_amdgcn_perm(d1, d0, 0x05010400u), k23a = __builtin_amdgcn_perm(d3, d2, 0x05010400u);
     const uint32_t k01b = __builtin_amdgcn_perm(d1, d0, 0x07030602u), k23b = __builtin_amdgcn_perm(d3, d2, 0x07030602u);
-    uint16_t* row = &vbuf[buf][(fvc * 8 + 4 * half) * VS + fvg * 4];
-    *reinterpret_cast<uint2*>(row) = make_uint2(KVChunk<true>::pair(k01a, false), KVChunk<true>::pair(k23a, false));
-    *reinterpret_cast<uint2*>(row + VS) = make_uint2(KVChunk<true>::pair(k01a, true), KVChunk<true>::pair(k23a, true));
-    *reinterpret_cast<uint2*>(row + 2 * VS) = make_uint2(KVChunk<true>::pair(k01b, false), KVChunk<true>::pair(k23b, false));
-    *reinterpret_cast<uint2*>(row + 3 * VS) = make_uint2(KVChunk<true>::pair(k01b, true), KVChunk<true>::pair(k23b, true));
+    const int r0 = fvc * 8 + 4 * half;
+    uint16_t* vb = &vbuf[buf][fvg * 4];
+    *reinterpret_cast<uint2*>(vb + vrow(r0)) = make_uint2(KVChunk<true>::pair(k01a, false), KVChunk<true>::pair(k23a, false));
+    *reinterpret_cast<uint2*>(vb + vrow(r0 + 1)) = make_uint2(KVChunk<true>::pair(k01a, true), KVChunk<true>::pair(k23a, true));
+    *reinterpret_cast<uint2*>(vb + vrow(r0 + 2)) = make_uint2(KVChunk<true>::pair(k01b, false), KVChunk<true>::pair(k23b, false));
+    *reinterpret_cast<uint2*>(vb + vrow(r0 + 3)) = make_uint2(KVChunk<true>::pair(k01b, true), KVChunk<true>::pair(k23b, true));
   };
   // V(j) to LDS: the codes are interleaved by key before decoding: one v_perm
   // puts channels c and c + 1 of keys 2i and 2i + 1 into one word, whose low
@@ -1079,7 +1097,7 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
   };
   // O^T += V^T P^T of a whole tile from vbuf[buf] (last tile only)
   auto pv_tile = [&](int buf, const uint32_t (&pw)[16]) {
-    const uint16_t* vf = &vbuf[buf][li * VS + hg * 8];
+    const uint16_t* vf = &vbuf[buf][vrow(li) + hg * 8];
 #pragma unroll
     for (int k4 = 0; k4 < 4; ++k4) {
       const bf16x8_t pf =
@@ -1087,7 +1105,7 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
 #pragma unroll
       for (int d = 0; d < DB; ++d)
         oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            *reinterpret_cast<const bf16x8_t*>(vf + d * 32 * VS + k4 * 16), pf, oacc[d], 0, 0, 0);
+            *reinterpret_cast<const bf16x8_t*>(vf + vrow(d * 32) + k4 * 16), pf, oacc[d], 0, 0, 0);
     }
   };
   // bf16: the tile loads go straight to LDS and are counted by vmcnt, so
@@ -1127,7 +1145,7 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
   // fp8 staging inside the slot program: one unit (a K row chunk, a V half,
   // a load) every kStageStride slots from kStageSlot0 on
   constexpr int kStageSlot0 = 0, kStageStride = 1;
-  const uint16_t* vf0 = &vbuf[0][li * VS + hg * 8];
+  const uint16_t* vf0 = &vbuf[0][vrow(li) + hg * 8];
   const uint16_t* kf0 = &kbuf[0][li * KS + hg * 8];
   auto tile = [&](int vb, int kbf, const f32x16_t (&scur)[2], f32x16_t (&snext)[2], const uint32_t (&pprev)[16],
                   uint32_t (&pcur)[16], float& ps0, float& ps1, float c, float neg_m, auto&& slot_work) {
@@ -1135,7 +1153,7 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
     const uint16_t* vf = vf0 + vb * VBUF;
     const uint16_t* kf = kf0 + kbf * KBUF;
     auto frag = [&](int t) -> bf16x8_t {
-      if (t < 4 * DB) return *reinterpret_cast<const bf16x8_t*>(vf + (t % DB) * 32 * VS + (t / DB) * 16);
+      if (t < 4 * DB) return *reinterpret_cast<const bf16x8_t*>(vf + vrow((t % DB) * 32) + (t / DB) * 16);
       const int u = t - 4 * DB;
       return *reinterpret_cast<const bf16x8_t*>(kf + (u & 1) * 32 * KS + (u >> 1) * 16);
     };

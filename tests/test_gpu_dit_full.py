@@ -100,11 +100,15 @@ def test_full_width_block_matches_oracle(dev):
     torch.cuda.synchronize()
     assert vo.shape == (B, LQ, cfg.out_channels) and ao.shape == (B, LA, cfg.out_channels)
     cv, ca = cosine(vo, ref_v), cosine(ao, ref_a)
-    print(f"full-width block: cosine video {cv:.6f} audio {ca:.6f}", flush=True)
-    assert cv >= 0.999 and ca >= 0.999, (cv, ca)
-    for out, ref in ((vo, ref_v), (ao, ref_a)):
-        err = (out.float().cpu() - ref).abs().max().item()
-        assert err <= 3e-2 * ref.abs().max().item(), err
+    rel = [((out.float().cpu() - ref).abs().max() / ref.abs().max()).item() for out, ref in ((vo, ref_v), (ao, ref_a))]
+    print(f"full-width block: cosine video {cv:.6f} audio {ca:.6f}; max-abs / max |ref| {rel[0]:.2e} {rel[1]:.2e}",
+          flush=True)
+    # bf16 activations and weights against the fp32 oracle: measured cosines
+    # 0.999975 / 0.999984 and largest errors 0.75 % / 0.43 % of the largest
+    # output, so the bars leave a 4x margin on 1 - cos and 2x on the error
+    assert cv >= 0.9999 and ca >= 0.9999, (cv, ca)
+    for r in rel:
+        assert r <= 1.5e-2, rel
     del model, caches
     gc.collect()
     torch.cuda.empty_cache()

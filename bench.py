@@ -223,6 +223,58 @@ def stream_bench(dev, n_chunks: int = 60, kv_dtype: str = "fp8", warm_chunks: in
                         "window | current chunk, whole layer per chunk (projections included)"}
 
 
+def c3_bench(dev, iters: int = 200) -> dict:
+    """The audio and cross-attention calls of one block at the chunk shape,
+    B = 2, inputs ~N(0, 1), seed 2: audio self-attention (75 queries, 32 x 64,
+    over 600 cached + 75 current audio keys), A2V (1152 video queries over the
+    chunk's 75 audio keys, 32 x 64), V2A (75 audio queries over the chunk's 1152
+    video keys, 32 x 64) and the text cross-attention (1152 queries, 32 x 128,
+    over 1024 text keys of which each row keeps its first 820: 20 % padding, the
+    per-row key counts of the pipelined kernel).  V is key-major, as the layer
+    stores it (arena, or the key-major copy of a plain-tensor cache).  Each call
+    timed back to back between HIP events; FLOPs count the attended keys."""
+    from taomate_amd import kernels
+    from taomate_amd.kernels import KVSegment
+    from taomate_amd.kv_cache import KVArena
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+
+    def rnd(*shape):
+        return torch.randn(*shape, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+
+    def arena_segs(lens, Hh, Dh):
+        a = KVArena(B, sum(lens) + 8 * len(lens), Hh, Dh, dev, "bf16", name="c3")
+        segs, pos = [], 0
+        for n in lens:
+            a.slots("k", pos, n).copy_(rnd(B, n, Hh, Dh))
+            a.slots("v", pos, n).copy_(rnd(B, n, Hh, Dh))
+            segs.append(KVSegment(a.slots("k", pos, n), a.slots("v", pos, n)))
+            pos += -(-n // 8) * 8
+        return a, segs
+
+    calls = {}
+    for name, lq, lens, Dh, klen in (("audio_self", 75, [600, 75], 64, None),
+                                     ("a2v", LQ, [75], 64, None),
+                                     ("v2a", 75, [LQ], 64, None),
+                                     ("text_cross", LQ, [1024], 128, [820, 820])):
+        a, segs = arena_segs(lens, H, Dh)
+        q = rnd(B, lq, H, Dh)
+        out = torch.empty_like(q)
+        fn = (lambda q=q, segs=segs, out=out, klen=klen: kernels.flash_attn(q, segs, out, key_lens=klen))
+        for _ in range(20):
+            fn()
+        ms = time_region(fn, iters)
+        keys = (sum(klen) / B) if klen else sum(lens)
+        fl = 4.0 * B * H * lq * keys * Dh
+        calls[name] = {"queries": lq, "keys": int(keys), "head_dim": Dh, "us": ms * 1e3,
+                       "TFLOP/s": fl / (ms * 1e-3) / 1e12, "frac_bf16_peak": fl / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
+        del a, segs, q, out
+    calls["what"] = ("B = 2, 32 heads; each call back to back between HIP events; small calls are bound by "
+                     "latency (launch and one round of loads), not by the matrix cores")
+    return calls
+
+
 def dit_bench(dev, steps: int = 5, warmup: int = 2, learned_memory: bool = False, fuse_qkv: bool = True):
     """One denoising step of the 48-block dual-stream model (video 32 x 128,
     d = 4096; audio 32 x 64, d = 2048; 4x GELU FFNs; AdaLN modulation) for one
@@ -609,6 +661,8 @@ def main():
     ap.add_argument("--attn-queries", type=int, default=LQ,
                     help="--attn-only: attend the chunk's first N queries (1024: 8 q-tiles per head, the pair kernel)")
     ap.add_argument("--no-fp8", action="store_true", help="skip the same step on the fp8-e4m3 arena (its own object)")
+    ap.add_argument("--no-c3", action="store_true",
+                    help="skip the audio self / A2V / V2A / text cross-attention calls (their own object)")
     ap.add_argument("--no-stream", action="store_true", help="skip the 60-chunk long-stream measurement")
     ap.add_argument("--stream-only", action="store_true", help="run only the 60-chunk long-stream measurement")
     ap.add_argument("--no-dit", action="store_true", help="skip the 48-block denoising-step measurement")
@@ -765,6 +819,8 @@ def main():
     }
     if args.kv == "bf16" and not args.no_fp8:
         res["fp8"] = fp8_step_bench(dev, args.steps, args.warmup, args.settle_seconds)
+    if args.kv == "bf16" and not args.no_c3:
+        res["c3"] = c3_bench(dev)
     if not args.no_stream:
         res["long_stream"] = stream_bench(dev, fuse_qkv=not args.no_fuse_qkv)
     if not args.no_dit:

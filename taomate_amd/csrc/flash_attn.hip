@@ -1449,20 +1449,25 @@ Slots resident_slots(int threads = 256) {
 // (194-196 against 200-202 us) while its per-tile barrier also waited for
 // the register-staged loads; without that wait it gains from one piece per
 // CU too (187.6 against 180.4 us).  The staged kernel's pieces fill every
-// slot.  Only worth it when there is at least one whole round
-// (otherwise the grid is a single partial round and the extra combine
-// launch costs more than it saves) and each piece keeps >= 4 key tiles.
+// slot.  Each piece keeps >= 4 key tiles behind a whole round.  A grid
+// that is a single partial round (fewer q-tiles than slots: the 75-query
+// audio and V2A calls, 64 q-tiles at B = 2 and 32 heads) is split too, into
+// pieces of >= 2 key tiles, so its few workgroups spread over the CUs: V2A
+// 75 x 1152 16.0 -> 12.5 us, audio self-attention 75 x 675 14.2 -> 12.6 us.
 // Zero tail tiles: no split.
 inline void plan_split(int64_t nq, int ntiles, Slots s, int64_t* n_full, int* split) {
   *n_full = nq;
   *split = 1;
   const int slots = s.slots;
-  if (slots <= 0 || nq < slots || nq % slots == 0) return;
+  if (slots <= 0 || nq % slots == 0) return;
   const int64_t full = (nq / slots) * slots;
   const int64_t tail = nq - full;
   int sp = (int)(s.pieces / tail);
   if (sp > kMaxSplit) sp = kMaxSplit;
-  if (sp > ntiles / 4) sp = ntiles / 4;
+  // pieces keep >= 4 key tiles behind a whole round, >= 2 when the grid is
+  // a single partial round (its few workgroups would leave most CUs idle)
+  const int min_tiles = full > 0 ? 4 : 2;
+  if (sp > ntiles / min_tiles) sp = ntiles / min_tiles;
   if (sp < 2) return;
   *n_full = full;
   *split = sp;

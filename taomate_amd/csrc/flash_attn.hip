@@ -791,18 +791,20 @@ struct KeyStreamT {
 // registers as they were (the framed state costs the D = 128 instance
 // register spills).
 //
-// PAIR (bf16): 8-wave workgroups of two groups of 4 waves (waves w and w + 4
+// PAIR: 8-wave workgroups of two groups of 4 waves (waves w and w + 4
 // share a SIMD) that own two q-tiles of one head (pair_work) and read one
-// K/V stream.  Only group 0 issues the tile loads, so group 1's waves run
-// their slot programs while group 0's wait on the load pipe, and the groups
-// meet at every per-tile barrier: the two waves of a SIMD finish together,
-// where two 4-wave workgroups on one CU do not (the older one's waves win
-// the issue arbitration and finish about a quarter earlier, leaving the CU
-// half busy until the other ends).
+// K/V stream.  bf16: only group 0 issues the tile loads, so group 1's waves
+// run their slot programs while group 0's wait on the load pipe.  fp8:
+// group 0 stages (loads and decodes) the K tiles and group 1 the V tiles,
+// so each thread stages half of what a 4-wave workgroup's does for the
+// same two q-tiles.  The groups meet at every per-tile barrier: the two
+// waves of a SIMD finish together, where two 4-wave workgroups on one CU do
+// not (the older one's waves win the issue arbitration and finish about a
+// quarter earlier, leaving the CU half busy until the other ends).
 template <int D, bool FP8, bool FRAMED, bool PAIR = false>
 __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
   static_assert(FP8 || !FRAMED, "frame tiling is an fp8 feature");
-  static_assert(!(PAIR && FP8), "pair workgroups are a bf16 feature");
+  static_assert(!(PAIR && FRAMED), "pair workgroups take the plain tiling");
   constexpr int BM = kBM, BN = kBN;
   constexpr int NKC = D / 8;
   constexpr int KS = D + 8;
@@ -965,18 +967,21 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
   constexpr int FROWS = 256 / NKC;
   constexpr int FKL = BN / FROWS;
   constexpr int NVP = (BN / 4) * NKC;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x & 255;  // thread index within the group
   const int fkc = tid % NKC, fkr = tid / NKC;
   const int fvg = tid % 16, fvc = tid / 16;
   const bool fv_on = tid < NVP;
+  const bool stage_k = !PAIR || grp == 0, stage_v = !PAIR || grp == 1;  // wave-uniform
   uint2 kreg[FP8 ? FKL : 1], vreg[FP8 ? 4 : 1];
   auto load_k8 = [&]() {
+    if (!stage_k) return;
     const auto rs = __builtin_amdgcn_make_buffer_rsrc((void*)kit.ptr, (short)0, kit.nvalid() * row_bytes, 0x00020000);
 #pragma unroll
     for (int i = 0; i < FKL; ++i) kreg[i] = KVChunk<true>::bload(rs, (fkr + FROWS * i) * row_bytes + fkc * 8);
     kit.next(p.k_ptr, k_head, k_tile, p);
   };
   auto load_v8 = [&]() {
+    if (!stage_v) return;
     const auto rs = __builtin_amdgcn_make_buffer_rsrc((void*)vit.ptr, (short)0, vit.nvalid() * row_bytes, 0x00020000);
     if (fv_on) {
 #pragma unroll
@@ -985,6 +990,7 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
     vit.next(p.v_ptr, v_head, v_tile, p);
   };
   auto store_k8_row = [&](int buf, int i) {
+    if (!stage_k) return;
     *reinterpret_cast<uint4*>(&kbuf[buf][sig(fkr + FROWS * i) * KS + fkc * 8]) = KVChunk<true>::to_bf16(kreg[i]);
   };
   auto store_k8 = [&](int buf) {
@@ -992,7 +998,7 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
     for (int i = 0; i < FKL; ++i) store_k8_row(buf, i);
   };
   auto store_v8_half = [&](int buf, int half) {
-    if (!fv_on) return;
+    if (!stage_v || !fv_on) return;
     const uint32_t d0 = half ? vreg[0].y : vreg[0].x, d1 = half ? vreg[1].y : vreg[1].x;
     const uint32_t d2 = half ? vreg[2].y : vreg[2].x, d3 = half ? vreg[3].y : vreg[3].x;
     // channels 4*half + {0, 1} and {2, 3} of keys (0, 1) and (2, 3)
@@ -1350,10 +1356,11 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_pipe_kernel(const FlashParam
   flash_pipe_body<D, FP8, false>(p);
 }
 
-// bf16 key-major V with an even number of q-tiles per head: pair workgroups
-template <int D>
+// bf16 key-major V, or fp8 K/V in frames of whole 64-key tiles, with an even
+// number of q-tiles per head: pair workgroups
+template <int D, bool FP8>
 __global__ void __launch_bounds__(512, 1) flash_fwd_pair_kernel(const FlashParams p) {
-  flash_pipe_body<D, false, false, true>(p);
+  flash_pipe_body<D, FP8, false, true>(p);
 }
 
 // fp8 frames that are not a whole number of 64-key tiles
@@ -1386,8 +1393,8 @@ int launch_flash_pipe(const FlashParams& p, hipStream_t st) {
   LTX_REQUIRE(nblocks <= 0x7FFFFFFF, "ltx_flash_attn_fwd: grid too large");
   if constexpr (FRAMED)
     hipLaunchKernelGGL((flash_fwd_pipe_framed_kernel<D>), dim3((unsigned)nblocks), dim3(256), 0, st, p);
-  else if (!FP8 && p.pair)
-    hipLaunchKernelGGL((flash_fwd_pair_kernel<D>), dim3((unsigned)nblocks), dim3(512), 0, st, p);
+  else if (p.pair)
+    hipLaunchKernelGGL((flash_fwd_pair_kernel<D, FP8>), dim3((unsigned)nblocks), dim3(512), 0, st, p);
   else
     hipLaunchKernelGGL((flash_fwd_pipe_kernel<D, FP8>), dim3((unsigned)nblocks), dim3(256), 0, st, p);
   LTX_LAUNCH_CHECK("ltx_flash_attn_fwd");
@@ -1479,19 +1486,22 @@ inline int64_t workspace_bytes_for(int64_t tail, int split, int64_t D) {
 
 // Resident slots of the kernel a call with head size D takes: for
 // key-major bf16 V (vkey) the pair kernel when the q-tiles per head are
-// even (pair), else the pipelined kernel; the pipelined kernel for fp8 K/V;
-// else the staged kernel (its masked instance for a key mask).
+// even (pair), else the pipelined kernel; for fp8 K/V the same choice (the
+// framed kernel shares the pipelined kernel's occupancy); else the staged
+// kernel (its masked instance for a key mask).
 inline Slots flash_slots(int64_t D, bool vkey, bool fp8, bool mask, bool pair) {
   Slots s;
   if (D == 128)
-    s = vkey && pair ? resident_slots<flash_fwd_pair_kernel<128>>(512)
+    s = vkey && pair ? resident_slots<flash_fwd_pair_kernel<128, false>>(512)
         : vkey       ? resident_slots<flash_fwd_pipe_kernel<128, false>>()
+        : fp8 && pair ? resident_slots<flash_fwd_pair_kernel<128, true>>(512)
         : fp8        ? resident_slots<flash_fwd_pipe_kernel<128, true>>()
         : mask       ? resident_slots<flash_fwd_kernel<128, false, true>>()
                      : resident_slots<flash_fwd_kernel<128, false, false>>();
   else
-    s = vkey && pair ? resident_slots<flash_fwd_pair_kernel<64>>(512)
+    s = vkey && pair ? resident_slots<flash_fwd_pair_kernel<64, false>>(512)
         : vkey       ? resident_slots<flash_fwd_pipe_kernel<64, false>>()
+        : fp8 && pair ? resident_slots<flash_fwd_pair_kernel<64, true>>(512)
         : fp8        ? resident_slots<flash_fwd_pipe_kernel<64, true>>()
         : mask       ? resident_slots<flash_fwd_kernel<64, false, true>>()
                      : resident_slots<flash_fwd_kernel<64, false, false>>();
@@ -1512,13 +1522,16 @@ extern "C" int ltx_flash_attn_workspace_size(int64_t B, int64_t Lq, int64_t H, i
   const int64_t nq = B * H * nqt;
   const bool pair = nqt % 2 == 0;
   int64_t need = 0;
-  for (int k = 0; k < 4; ++k) {
-    const bool kp = k == 1 && pair;
+  // kernels: staged, pipelined (key-major V), fp8 pipelined (framed or
+  // not), fp8 pair (frames of whole tiles), masked staged
+  for (int k = 0; k < 5; ++k) {
+    const bool vk = k == 1, f8 = k == 2 || k == 3, mk = k == 4;
+    const bool kp = (k == 1 || k == 3) && pair;
     const int64_t nu = kp ? nq / 2 : nq;
     int64_t n_full;
     int split;
     // with an unbounded key count the planned split is the largest any call of this shape plans
-    plan_split(nu, 1 << 30, flash_slots(D, k == 1, k == 2, k == 3, pair), &n_full, &split);
+    plan_split(nu, 1 << 30, flash_slots(D, vk, f8, mk, kp), &n_full, &split);
     const int64_t b = split > 1 ? workspace_bytes_for((nu - n_full) * (kp ? 2 : 1), split, D) : 0;
     need = b > need ? b : need;
   }
@@ -1640,13 +1653,13 @@ static int flash_attn_fwd_impl(const void* q, int64_t B, int64_t Lq, int64_t H, 
   LTX_REQUIRE(n > 0, "ltx_flash_attn_fwd: no keys (Lk == 0)");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   // balanced tail (needs a workspace; without one every q-tile runs whole).
-  // Key-major bf16 V with an even number of q-tiles per head runs the pair
-  // kernel, whose grid counts units of two q-tiles (two partial results per
-  // split unit).
+  // Key-major bf16 V, or fp8 K/V in frames of whole 64-key tiles, with an
+  // even number of q-tiles per head runs the pair kernel, whose grid counts
+  // units of two q-tiles (two partial results per split unit).
   {
     const int64_t nq = (int64_t)B * H * p.n_qtiles;
     LTX_REQUIRE(nq <= 0x7FFFFFFF, "ltx_flash_attn_fwd: grid too large");
-    p.pair = vkey && p.n_qtiles % 2 == 0 ? 1 : 0;
+    p.pair = (vkey || (fp8 && frame_tokens % kBN == 0)) && p.n_qtiles % 2 == 0 ? 1 : 0;
     const int64_t nu = p.pair ? nq / 2 : nq;
     const int per_unit = p.pair ? 2 : 1;
     int64_t n_full = nu;

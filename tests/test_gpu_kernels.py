@@ -504,14 +504,21 @@ def test_flash_attn_key_mask(dev):
                                   (1, 128, 4, 128, 64, [64]),
                                   (1, 128, 4, 128, 64, [128]),
                                   (1, 128, 4, 128, 64, [192]),
-                                  (2, 96, 4, 64, 64, [64, 64, 64])],
+                                  (2, 96, 4, 64, 64, [64, 64, 64]),
+                                  (2, 1280, 32, 128, 384, [384, 768, 1152]),
+                                  (1, 1024, 8, 64, 64, [256, 512, 1024])],
                          ids=["16x24grid", "64tok_frames", "8x12grid_96tok_frames", "8x12grid_96tok_D128",
-                              "audio_25tok_frames", "1_tile", "2_tiles", "3_tiles", "3_segments_of_1_tile"])
+                              "audio_25tok_frames", "1_tile", "2_tiles", "3_tiles", "3_segments_of_1_tile",
+                              "pair_split_tail_1280q", "pair_one_round_D64"])
 def test_flash_attn_fp8_kv(dev, case):
     """fp8 K/V with one scale per (batch, head, frame); frames of 96 and 25
     tokens are cut into 64-key tiles at frame boundaries (64 + 32, and one
     partial tile per frame).  One to three key tiles exercise the staging
-    prologue and the last iterations of the tile loop."""
+    prologue and the last iterations of the tile loop.  Even q-tile counts
+    with frames of whole tiles take the pair workgroups (group 0 stages K,
+    group 1 V): 1280 queries at B = 2 and 32 heads give 320 units, 256 whole
+    and 64 cut into key ranges and merged; 1024 queries over 8 heads one
+    partial round."""
     B, Lq, H, D, frame, lens = case
     g = gen(9)
     q = randn((B, Lq, H, D), g, torch.bfloat16)

@@ -59,3 +59,42 @@ def test_noalloc_matches_workspace_entry_point(dev, first, second):
         assert torch.equal(lse, ref_lse), f"call {i}: noalloc lse differs"
         if i == 0:
             assert_bf16_close(out, _ref_attn(q.cpu(), K, V), "noalloc vs fp32")
+
+
+def _fp8_segments(dev, B, H, D, lens, frame, g):
+    """fp8 K/V spans (frame-aligned, codes and per-frame scales) and the
+    dequantised K/V they hold."""
+    from oracle import fp8 as OF
+    n = sum(lens)
+    kc, ksc = OF.quantize_kv(randn((B, n, H, D), g, torch.float32), frame)
+    vc, vsc = OF.quantize_kv(randn((B, n, H, D), g, torch.float32), frame)
+    kcd, vcd, kscd, vscd = kc.to(dev), vc.to(dev), ksc.to(dev), vsc.to(dev)
+    segs, pos = [], 0
+    for m in lens:   # spans of one store (shared strides), whole frames each
+        f0, nf = pos // frame, m // frame
+        segs.append(KVSegment(kcd[:, pos:pos + m], vcd[:, pos:pos + m], kscd[:, :, f0:f0 + nf],
+                              vscd[:, :, f0:f0 + nf]))
+        pos += m
+    return segs, OF.dequantize_kv(kc, ksc, frame), OF.dequantize_kv(vc, vsc, frame)
+
+
+@pytest.mark.parametrize("first,second", [
+    # fp8 K/V in 384-token frames, even q-tile counts per head (the pair
+    # workgroups: group 0 stages K, group 1 V): 320 then 280 units on 256
+    ((2, 1280, 32, 128, [384, 768, 1152]), (1, 1792, 40, 128, [384, 1152])),
+])
+def test_noalloc_fp8_pair_matches_workspace_entry_point(dev, first, second):
+    g = gen(22)
+    frame = 384
+    for i, (B, Lq, H, D, lens) in enumerate((first, second)):
+        print(f"noalloc fp8 call {i}: B={B} Lq={Lq} H={H} D={D} keys={lens}", flush=True)
+        segs, K, V = _fp8_segments(dev, B, H, D, lens, frame, g)
+        q = randn((B, Lq, H, D), g, torch.bfloat16).to(dev)
+        ref_out = torch.empty(B, Lq, H, D, dtype=torch.bfloat16, device=dev)
+        out = torch.full((B, Lq, H, D), float("nan"), dtype=torch.bfloat16, device=dev)
+        kernels.flash_attn(q, segs, ref_out, frame_tokens=frame)
+        kernels.flash_attn(q, segs, out, frame_tokens=frame, noalloc=True)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref_out), f"call {i}: noalloc output differs from the workspace entry point"
+        if i == 0:
+            assert_bf16_close(out, _ref_attn(q.cpu(), K, V), "noalloc fp8 vs the dequantised cache")

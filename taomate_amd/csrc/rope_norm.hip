@@ -191,14 +191,18 @@ __global__ void __launch_bounds__(256) rope_table_video_kernel(
 // The video table of a new start frame from a table of the same grid (any
 // start frame).  Only the t-axis entries depend on the start frame: the h and
 // w entries of token (f, r, c) are those of (r, c) in every frame, and the pad
-// entries are the identity.  One workgroup per (frame, head, block of
-// kRopeRows rows) computes its frame's t-axis cos/sin with the float32
+// entries are the identity.  One workgroup per (frame, head, token row of
+// the grid) computes its frame's t-axis cos/sin with the float32
 // operations of rope_table_kernel (so every entry is bit-identical to a fresh
 // build) and streams the rows: 16-byte loads of the source entries, the
 // t-axis ones replaced, 16-byte stores.  A long stream builds one 3-frame
 // table per chunk; this reads and writes it instead of evaluating the h and w
-// angles again.
+// angles again.  A workgroup lives about one memory round trip, so the
+// table is cut into many small workgroups (1536 for a 3-frame 16x24 chunk of
+// 32 heads, all resident at once) rather than a few long ones.
 // ---------------------------------------------------------------------------
+constexpr int kRetimeRows = 1;
+
 template <typename TOut>
 __global__ void __launch_bounds__(256) rope_table_retime_kernel(
     TOut* __restrict__ cos_out, TOut* __restrict__ sin_out, const TOut* __restrict__ cos_src,
@@ -206,8 +210,8 @@ __global__ void __launch_bounds__(256) rope_table_retime_kernel(
     int64_t start_frame, float max_t, int half_dim, int heads, int64_t T) {
   extern __shared__ float tfac[];  // [P][2]: this frame's t-axis cos / sin (other entries unused)
   const int f = blockIdx.x, h = blockIdx.y;
-  const int r0 = blockIdx.z * kRopeRows;
-  const int nr = min(kRopeRows, grid_h - r0);
+  const int r0 = blockIdx.z * kRetimeRows;
+  const int nr = min(kRetimeRows, grid_h - r0);
   const int P = half_dim / heads;
   const int pad = half_dim - n_freq * 3;
   constexpr int V = 16 / sizeof(TOut);  // entries per 16-byte vector
@@ -717,7 +721,7 @@ extern "C" int ltx_rope_table_retime(void* cos_out, void* sin_out, const void* c
   const int64_t T = grid_f * grid_h * grid_w;
   if (T == 0) return LTX_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const dim3 vgrid((unsigned)grid_f, (unsigned)num_heads, (unsigned)ceil_div(grid_h, kRopeRows));
+  const dim3 vgrid((unsigned)grid_f, (unsigned)num_heads, (unsigned)ceil_div(grid_h, kRetimeRows));
   const size_t lds = (size_t)P * 2 * sizeof(float);
   if (out_dtype == LTX_BF16)
     hipLaunchKernelGGL(rope_table_retime_kernel<uint16_t>, vgrid, dim3(256), lds, st, (uint16_t*)cos_out,

@@ -282,8 +282,10 @@ def dit_bench(dev, steps: int = 5, warmup: int = 2, learned_memory: bool = False
     chunk workload above, 75 audio tokens over 600 cached, 1024 text tokens
     (20 % masked) for both streams, A2V / V2A over the chunk's own tokens.
     Random bf16 weights (seed 3), sigma ~ U(0, 1).  Timed with HIP events
-    around whole steps; the attention share is the summed duration of every
-    attention call (events around each, same stream) over the step time.
+    around whole steps, with the audio ops on their own stream (the model's
+    default) and again on one stream; the attention share is the summed
+    duration of every attention call (events around each, one stream) over
+    the one-stream step time.
     With ``learned_memory`` every 4th block carries the memory adapters
     (video 8 x 64 over 48 tokens + colour FiLM, audio 8 x 32 over 64 tokens),
     fed by a StreamingMemory updated once with the chunk's latents."""
@@ -363,7 +365,19 @@ def dit_bench(dev, steps: int = 5, warmup: int = 2, learned_memory: bool = False
         e1.synchronize()
         ms = e0.elapsed_time(e1) / steps
         finite = bool(torch.isfinite(vo).all() and torch.isfinite(ao).all())
-        # attention share: three more steps with events around every attention
+        # the same steps with every op on one stream (the audio stream's
+        # kernels between the video stream's instead of beside them)
+        model.overlap_audio_(False)
+        for _ in range(warmup):
+            step()
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        e1.synchronize()
+        ms_one = e0.elapsed_time(e1) / steps
+        # attention share (one stream, so that each call's events hold only
+        # that call): three more steps with events around every attention
         # call; the fastest of them (a host stall only lengthens a step) gives
         # the step time and its attention calls' summed time
         kernels.flash_attn = timed_flash
@@ -380,6 +394,7 @@ def dit_bench(dev, steps: int = 5, warmup: int = 2, learned_memory: bool = False
                 best = cur if best is None or cur[0] < best[0] else best
         finally:
             kernels.flash_attn = real_flash
+            model.overlap_audio_(True)
         ms_inst, ms_attn, n_attn = best
         # the same steps with the text cross-attention's K/V kept across steps
         # (the reference's exact text K/V cache, off by default there and in
@@ -395,6 +410,8 @@ def dit_bench(dev, steps: int = 5, warmup: int = 2, learned_memory: bool = False
         ms_tkv = e0.elapsed_time(e1) / steps
         model.cache_text_kv_(False)
     res = {"ms_per_step": ms, "chunk_query_tokens_per_s": B * LQ / (ms * 1e-3), "params": n_params,
+           "audio_stream": "the audio ops on a second HIP stream beside the video ops (overlap_audio_)",
+           "ms_per_step_one_stream": ms_one,
            "ms_per_step_text_kv_cached": ms_tkv,
            "attention_ms": ms_attn, "attention_share": ms_attn / ms_inst, "attention_calls": n_attn,
            "outputs_finite": finite, "learned_memory": learned_memory,

@@ -163,3 +163,43 @@ def test_48_block_step_properties(dev):
     del model, caches, committed, kept
     gc.collect()
     torch.cuda.empty_cache()
+
+
+@pytest.mark.timeout(900)
+def test_audio_stream_overlap_bit_identical(dev):
+    """forward_chunk with the audio ops on their own HIP stream
+    (AVModel.overlap_audio_) gives the one-stream outputs and committed
+    caches bit for bit: 4 full-width blocks, a denoise step then a clean
+    commit, each on fresh caches, the overlapped pass run twice."""
+    cfg = D.AVConfig(num_layers=4)
+    model = D.build_model(cfg, dev, seed=3).fuse_qkv_()
+    x = _inputs(cfg, 63, 1)
+    dense = x["cache"] * cfg.num_layers
+    bf = lambda t: t.to(dev, torch.bfloat16)
+    args = (bf(x["video"]), bf(x["audio"]), x["sigma"].to(dev), bf(x["vctx"]), bf(x["actx"]), bf(x["mask"]),
+            bf(x["mask"]), *_pes(cfg, dev))
+    fields = ("video_self_k", "video_self_v", "audio_self_k", "audio_self_v", "a2v_k", "a2v_v", "v2a_k", "v2a_v")
+
+    def run(overlap):
+        model.overlap_audio_(overlap)
+        caches = _arena_caches(dev, cfg, dense)
+        with torch.no_grad():
+            vo, ao, _ = model.forward_chunk(*args, caches)
+            _, _, committed = model.forward_chunk(*args[:2], torch.zeros_like(args[2]), *args[3:], caches,
+                                                  kv_cache_only=True)
+        torch.cuda.synchronize()
+        dense_of = lambda t: t.materialize() if hasattr(t, "materialize") else t.clone()
+        return vo, ao, [[dense_of(getattr(c, f)) for f in fields] for c in committed]
+
+    ref = run(False)
+    for i in range(2):
+        print(f"audio stream overlap: pass {i}", flush=True)
+        got = run(True)
+        assert torch.equal(got[0], ref[0]) and torch.equal(got[1], ref[1]), f"pass {i}: outputs differ"
+        for layer, (g, r) in enumerate(zip(got[2], ref[2])):
+            for f, a, b in zip(fields, g, r):
+                assert torch.equal(a, b), f"pass {i}: layer {layer} {f} differs"
+    model.overlap_audio_(False)
+    del model
+    gc.collect()
+    torch.cuda.empty_cache()

@@ -353,29 +353,24 @@ def dit_bench(dev, steps: int = 5, warmup: int = 2, learned_memory: bool = False
         return model.forward_chunk(vlat, alat, sigma, vctx, actx, mask, mask, vpe, ape, vcross, across, caches,
                                    **mem)
 
-    with torch.no_grad():
+    def timed_steps():
         for _ in range(warmup):
             step()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(steps):
-            vo, ao, _ = step()
+            out = step()
         e1.record()
         e1.synchronize()
-        ms = e0.elapsed_time(e1) / steps
-        finite = bool(torch.isfinite(vo).all() and torch.isfinite(ao).all())
-        # the same steps with every op on one stream (the audio stream's
-        # kernels between the video stream's instead of beside them)
+        return e0.elapsed_time(e1) / steps, out
+
+    with torch.no_grad():
+        # every op on one stream first (the audio stream's kernels between the
+        # video stream's), then the model's default with the audio ops beside
+        # them on their own stream
         model.overlap_audio_(False)
-        for _ in range(warmup):
-            step()
-        e0.record()
-        for _ in range(steps):
-            step()
-        e1.record()
-        e1.synchronize()
-        ms_one = e0.elapsed_time(e1) / steps
+        ms_one, _ = timed_steps()
         # attention share (one stream, so that each call's events hold only
         # that call): three more steps with events around every attention
         # call; the fastest of them (a host stall only lengthens a step) gives
@@ -396,18 +391,13 @@ def dit_bench(dev, steps: int = 5, warmup: int = 2, learned_memory: bool = False
             kernels.flash_attn = real_flash
             model.overlap_audio_(True)
         ms_inst, ms_attn, n_attn = best
+        ms, (vo, ao, _) = timed_steps()
+        finite = bool(torch.isfinite(vo).all() and torch.isfinite(ao).all())
         # the same steps with the text cross-attention's K/V kept across steps
         # (the reference's exact text K/V cache, off by default there and in
         # the figure above): the first call projects, the timed ones reuse
         model.cache_text_kv_()
-        step()
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(steps):
-            step()
-        e1.record()
-        e1.synchronize()
-        ms_tkv = e0.elapsed_time(e1) / steps
+        ms_tkv, _ = timed_steps()
         model.cache_text_kv_(False)
     res = {"ms_per_step": ms, "chunk_query_tokens_per_s": B * LQ / (ms * 1e-3), "params": n_params,
            "audio_stream": "the audio ops on a second HIP stream beside the video ops (overlap_audio_)",

@@ -661,17 +661,20 @@ class AVModel(nn.Module):
                       *_tensors(audio_cross_pe), *_tensors(video_cross_pe)):
                 if isinstance(t, torch.Tensor) and t.is_cuda:
                     t.record_stream(astream)
-        for blk, cache, blk_ada in zip(self.transformer_blocks, caches, ada):
-            vx, ax, nc = block_forward_with_cache(blk, vx, ax, v_ts, a_ts, video_pe, audio_pe, video_cross_pe,
-                                                  audio_cross_pe, video_ctx, audio_ctx, video_mask, audio_mask,
-                                                  v_ss, v_gate, a_ss, a_gate, cache, vm, am, cm, ada=blk_ada,
-                                                  v_prompt=v_prompt, a_prompt=a_prompt, audio_stream=astream)
-            new_caches.append(nc if commit else cache)
-            del nc
-        if astream is not None:
-            # join: the current stream waits for the audio stream's last block
-            main.wait_stream(astream)
-            ax.record_stream(main)
+        try:
+            for blk, cache, blk_ada in zip(self.transformer_blocks, caches, ada):
+                vx, ax, nc = block_forward_with_cache(blk, vx, ax, v_ts, a_ts, video_pe, audio_pe, video_cross_pe,
+                                                      audio_cross_pe, video_ctx, audio_ctx, video_mask, audio_mask,
+                                                      v_ss, v_gate, a_ss, a_gate, cache, vm, am, cm, ada=blk_ada,
+                                                      v_prompt=v_prompt, a_prompt=a_prompt, audio_stream=astream)
+                new_caches.append(nc if commit else cache)
+                del nc
+        finally:
+            if astream is not None:
+                # join (also when a block raised): the current stream waits
+                # for everything queued on the audio stream
+                main.wait_stream(astream)
+                ax.record_stream(main)
         if kv_cache_only:
             return None, None, new_caches
         vo = self._process_output(self.scale_shift_table, self.norm_out, self.proj_out, vx, v_emb)

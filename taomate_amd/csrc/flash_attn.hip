@@ -998,18 +998,20 @@ __device__ __forceinline__ void flash_pipe_body(const FlashParams& p) {
     for (int i = 0; i < FKL; ++i) store_k8_row(buf, i);
   };
   auto store_v8_half = [&](int buf, int half) {
-    if (!stage_v || !fv_on) return;
-    const uint32_t d0 = half ? vreg[0].y : vreg[0].x, d1 = half ? vreg[1].y : vreg[1].x;
-    const uint32_t d2 = half ? vreg[2].y : vreg[2].x, d3 = half ? vreg[3].y : vreg[3].x;
-    // channels 4*half + {0, 1} and {2, 3} of keys (0, 1) and (2, 3)
-    const uint32_t k01a = __builtin_amdgcn_perm(d1, d0, 0x05010400u), k23a = __builtin_amdgcn_perm(d3, d2, 0x05010400u);
-    const uint32_t k01b = __builtin_amdgcn_perm(d1, d0, 0x07030602u), k23b = __builtin_amdgcn_perm(d3, d2, 0x07030602u);
-    const int r0 = fvc * 8 + 4 * half;
-    uint16_t* vb = &vbuf[buf][fvg * 4];
-    *reinterpret_cast<uint2*>(vb + vrow(r0)) = make_uint2(KVChunk<true>::pair(k01a, false), KVChunk<true>::pair(k23a, false));
-    *reinterpret_cast<uint2*>(vb + vrow(r0 + 1)) = make_uint2(KVChunk<true>::pair(k01a, true), KVChunk<true>::pair(k23a, true));
-    *reinterpret_cast<uint2*>(vb + vrow(r0 + 2)) = make_uint2(KVChunk<true>::pair(k01b, false), KVChunk<true>::pair(k23b, false));
-    *reinterpret_cast<uint2*>(vb + vrow(r0 + 3)) = make_uint2(KVChunk<true>::pair(k01b, true), KVChunk<true>::pair(k23b, true));
+    if constexpr (FP8) {   // vreg holds the four staged code chunks only in the fp8 instances
+      if (!stage_v || !fv_on) return;
+      const uint32_t d0 = half ? vreg[0].y : vreg[0].x, d1 = half ? vreg[1].y : vreg[1].x;
+      const uint32_t d2 = half ? vreg[2].y : vreg[2].x, d3 = half ? vreg[3].y : vreg[3].x;
+      // channels 4*half + {0, 1} and {2, 3} of keys (0, 1) and (2, 3)
+      const uint32_t k01a = __builtin_amdgcn_perm(d1, d0, 0x05010400u), k23a = __builtin_amdgcn_perm(d3, d2, 0x05010400u);
+      const uint32_t k01b = __builtin_amdgcn_perm(d1, d0, 0x07030602u), k23b = __builtin_amdgcn_perm(d3, d2, 0x07030602u);
+      const int r0 = fvc * 8 + 4 * half;
+      uint16_t* vb = &vbuf[buf][fvg * 4];
+      *reinterpret_cast<uint2*>(vb + vrow(r0)) = make_uint2(KVChunk<true>::pair(k01a, false), KVChunk<true>::pair(k23a, false));
+      *reinterpret_cast<uint2*>(vb + vrow(r0 + 1)) = make_uint2(KVChunk<true>::pair(k01a, true), KVChunk<true>::pair(k23a, true));
+      *reinterpret_cast<uint2*>(vb + vrow(r0 + 2)) = make_uint2(KVChunk<true>::pair(k01b, false), KVChunk<true>::pair(k23b, false));
+      *reinterpret_cast<uint2*>(vb + vrow(r0 + 3)) = make_uint2(KVChunk<true>::pair(k01b, true), KVChunk<true>::pair(k23b, true));
+    }
   };
   // V(j) to LDS: the codes are interleaved by key before decoding: one v_perm
   // puts channels c and c + 1 of keys 2i and 2i + 1 into one word, whose low

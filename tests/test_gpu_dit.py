@@ -335,3 +335,75 @@ def test_ltx23_text_adaln_matches_oracle(dev, per_frame):
     for out, ref in ((vo, ref_v), (ao, ref_a)):
         err = (out.float().cpu() - ref).abs().max().item()
         assert err <= 3e-2 * ref.abs().max().item(), err
+
+
+def _small_arena_caches(dev, cfg, x):
+    hw = GH * GW
+    specs = {"video_self": T.ArenaSpec((NCACHE_F + 2 * NF) * hw, cfg.video_heads, cfg.video_d_head),
+             "audio_self": T.ArenaSpec(LA_CACHE + 2 * LA + 16, cfg.audio_heads, cfg.audio_d_head)}
+    kvc = T.init_kv_cache(cfg.num_layers, B, specs, dev)
+    caches = []
+    for lay, c in zip(kvc.layers, x["cache"]):
+        va, aa = lay.video_self_k.arena, lay.audio_self_k.arena
+        nv, na = c["video_self_k"].shape[1], c["audio_self_k"].shape[1]
+        va.slots("k", 0, nv).copy_(c["video_self_k"].to(dev, torch.bfloat16))
+        va.slots("v", 0, nv).copy_(c["video_self_v"].to(dev, torch.bfloat16))
+        aa.slots("k", 0, na).copy_(c["audio_self_k"].to(dev, torch.bfloat16))
+        aa.slots("v", 0, na).copy_(c["audio_self_v"].to(dev, torch.bfloat16))
+        caches.append(T.LayerKVCache(video_self_k=KVSpanView(va, "k", [(0, nv)]),
+                                     video_self_v=KVSpanView(va, "v", [(0, nv)]),
+                                     audio_self_k=KVSpanView(aa, "k", [(0, na)]),
+                                     audio_self_v=KVSpanView(aa, "v", [(0, na)])))
+    return caches
+
+
+@pytest.mark.parametrize("mode", [None, "cross_attn_adapter", "memory_kv_side_branch"])
+@pytest.mark.parametrize("per_frame", [False, True], ids=["per_sample_sigma", "per_frame_sigma"])
+def test_audio_stream_overlap_bit_identical(dev, mode, per_frame):
+    """The audio ops on their own stream (the model's default) against one
+    stream, bit for bit: outputs of a denoise step and the caches a clean
+    commit leaves, with and without learned-memory adapters (both
+    placements), with one sigma per sample (every block's modulation values
+    precomputed) and one per latent frame (each block computes its own on its
+    stream); the overlapped pass runs twice."""
+    mem_on = mode is not None
+    cfg = D.AVConfig(num_layers=2, video_dim=512, audio_dim=256, video_heads=8, audio_heads=4, video_d_head=64,
+                     audio_d_head=64, learned_memory_enabled=mem_on,
+                     learned_memory_mode=mode or "cross_attn_adapter", learned_memory_layer_interval=2,
+                     learned_memory_color_film_enabled=mem_on)
+    model = D.build_model(cfg, dev, seed=6)
+    x = _inputs(cfg)
+    g = torch.Generator().manual_seed(45)
+    bf = lambda t: t.to(dev, torch.bfloat16)
+    kw = {}
+    if mem_on:
+        kw = dict(learned_memory_video=bf(torch.randn(B, 48, cfg.in_channels, generator=g)),
+                  learned_memory_audio=bf(torch.randn(B, 64, cfg.in_channels, generator=g)),
+                  learned_memory_color=bf(torch.randn(B, 512, generator=g) * 0.5))
+    if per_frame:
+        sigma = torch.rand(B, NF, generator=g).to(dev)
+        kw["audio_sigma"] = torch.rand(B, generator=g).to(dev)
+    else:
+        sigma = x["sigma"].to(dev)
+    args = (bf(x["video"]), bf(x["audio"]), sigma, bf(x["vctx"]), bf(x["actx"]), bf(x["mask"]), bf(x["mask"]),
+            *_pes(dev, cfg))
+    fields = ("video_self_k", "video_self_v", "audio_self_k", "audio_self_v", "a2v_k", "a2v_v", "v2a_k", "v2a_v")
+
+    def run(overlap):
+        model.overlap_audio_(overlap)
+        caches = _small_arena_caches(dev, cfg, x)
+        with torch.no_grad():
+            vo, ao, _ = model.forward_chunk(*args, caches, **kw)
+            _, _, committed = model.forward_chunk(*args[:2], torch.zeros_like(sigma), *args[3:], caches,
+                                                  kv_cache_only=True, **kw)
+        torch.cuda.synchronize()
+        dense_of = lambda t: t.materialize() if hasattr(t, "materialize") else t.clone()
+        return vo, ao, [[dense_of(getattr(c, f)) for f in fields] for c in committed]
+
+    ref = run(False)
+    for i in range(2):
+        got = run(True)
+        assert torch.equal(got[0], ref[0]) and torch.equal(got[1], ref[1]), f"pass {i}: outputs differ"
+        for layer, (gl, rl) in enumerate(zip(got[2], ref[2])):
+            for f, a, b in zip(fields, gl, rl):
+                assert torch.equal(a, b), f"pass {i}: layer {layer} {f} differs"

@@ -9,7 +9,12 @@ implementation:
   partial and the merge by 2 exactly, so the bf16 output doubles bit for bit;
 * attention is linear in V for fixed Q and K;
 * a batch row computed alone (a grid with no split tail) equals the same row
-  of the two-row call (split tail and merge) up to rounding.
+  of the two-row call (split tail and merge) up to rounding;
+* attention depends on the set of keys, not on their order: reversed
+  segments give the same output up to rounding;
+* every key twice halves each weight and leaves the output as it was;
+* one vector added to every key shifts all of a query's logits by the same
+  amount, which the softmax removes.
 """
 import pytest
 import torch
@@ -126,3 +131,70 @@ def test_batch_row_alone_matches_two_row_call(dev):
     print(f"batch row alone vs in the pair: max-abs {mx:.3e} mean-abs {mn:.3e}", flush=True)
     # measured 9.8e-4 / 1.1e-5: bounds with a 4x margin
     assert mx <= 4e-3 and mn <= 5e-5, (mx, mn)
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+def test_segment_order_does_not_matter(dev, kv):
+    """Attention is a function of the key set: the four segments (whole
+    frames each) in reverse order give the same output up to the order of the
+    fp32 sums and of the running maximum's updates."""
+    B, H, D = 2, 32, 128
+    g = gen(44)
+    q = randn((B, LQ, H, D), g, torch.bfloat16).to(dev)
+    ks, vs = _parts(g, B, H, D)
+    vs = [v.to(torch.bfloat16) for v in vs]
+    fwd = _attend(dev, kv, q, ks, vs, H, D)
+    rev = _attend(dev, kv, q, ks[::-1], vs[::-1], H, D)
+    mx, mn = diff_stats(rev, fwd)
+    scale = fwd.float().abs().max().item()
+    print(f"segment order ({kv}): max-abs {mx:.3e} mean-abs {mn:.3e} scale {scale:.3e}", flush=True)
+    assert torch.isfinite(fwd.float()).all()
+    # measured (both K/V types) max-abs 9.8e-4 and mean-abs 4.3e-5 at a largest output of 0.17
+    assert cosine(rev, fwd) >= 0.99999 and mx <= 2 ** -6 * scale and mn <= 2 ** -11 * scale, (mx, mn, scale)
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+def test_duplicated_keys_leave_output_unchanged(dev, kv):
+    """Every key twice (eight segments: the four, then the four again): each
+    softmax weight halves and the output is the same, up to rounding; the
+    row sums reach twice the single set's."""
+    B, H, D = 2, 32, 128
+    g = gen(45)
+    q = randn((B, LQ, H, D), g, torch.bfloat16).to(dev)
+    ks, vs = _parts(g, B, H, D)
+    vs = [v.to(torch.bfloat16) for v in vs]
+    once = _attend(dev, kv, q, ks, vs, H, D)
+    twice = _attend(dev, kv, q, ks + ks, vs + vs, H, D)
+    mx, mn = diff_stats(twice, once)
+    scale = once.float().abs().max().item()
+    print(f"duplicated keys ({kv}): max-abs {mx:.3e} mean-abs {mn:.3e} scale {scale:.3e}", flush=True)
+    # measured max-abs 4.9e-4 (bf16) / 9.8e-4 (fp8), mean-abs 6.1e-6, at a largest output of 0.25
+    assert cosine(twice, once) >= 0.99999 and mx <= 2 ** -6 * scale and mn <= 2 ** -11 * scale, (mx, mn, scale)
+
+
+def test_uniform_logit_offset_leaves_output_unchanged(dev):
+    """K + u for one vector u shared by every key adds q.u to all of a query's
+    logits, which the softmax removes.  K and u sit on a 1/16 grid small
+    enough that K + u is exact in bf16, and u is large (6 to 8 per channel,
+    random signs), so a query's logits move by about 10 log2 units on
+    average and by over 40 at the extremes."""
+    B, H, D = 2, 32, 128
+    g = gen(46)
+    q = randn((B, LQ, H, D), g, torch.bfloat16).to(dev)
+    lens = [f * FRAME for f in SEG_FRAMES] + [LQ]
+    ks = [(torch.randint(-64, 65, (B, n, H, D), generator=g).float() / 16).to(torch.bfloat16) for n in lens]
+    vs = [randn((B, n, H, D), g, torch.bfloat16) for n in lens]
+    u = (torch.randint(96, 129, (1, 1, H, D), generator=g).float() / 16) * torch.where(
+        torch.rand(1, 1, H, D, generator=g) < 0.5, -1.0, 1.0)
+    ku = [(k.float() + u).to(torch.bfloat16) for k in ks]
+    assert all(torch.equal(a.float(), k.float() + u) for a, k in zip(ku, ks)), "K + u must be exact"
+    base = _attend(dev, "bf16", q, ks, vs, H, D)
+    moved = _attend(dev, "bf16", q, ku, vs, H, D)
+    off = (q.float().cpu() * u).sum(-1) / D ** 0.5 / torch.log(torch.tensor(2.0))
+    mx, mn = diff_stats(moved, base)
+    scale = base.float().abs().max().item()
+    print(f"logit offset up to {off.abs().max().item():.1f} (log2): max-abs {mx:.3e} mean-abs {mn:.3e} "
+          f"scale {scale:.3e}", flush=True)
+    assert off.abs().max().item() > 20.0
+    # measured max-abs 3.9e-3 and mean-abs 3.3e-7 at a largest output of 2.9 (offsets up to 43)
+    assert cosine(moved, base) >= 0.99999 and mx <= 2 ** -6 * scale and mn <= 2 ** -11 * scale, (mx, mn, scale)

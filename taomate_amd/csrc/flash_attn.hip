@@ -1486,6 +1486,8 @@ inline int64_t workspace_bytes_for(int64_t tail, int split, int64_t D) {
   return tail * split * kBM * (2 * 4 + D * 2);  // (max, sum) fp32 + bf16 O row
 }
 
+inline int64_t round256(int64_t x) { return (x + 255) / 256 * 256; }
+
 // Resident slots of the kernel a call with head size D takes: for
 // key-major bf16 V (vkey) the pair kernel when the q-tiles per head are
 // even (pair), else the pipelined kernel; for fp8 K/V the same choice (the
@@ -1513,6 +1515,49 @@ inline Slots flash_slots(int64_t D, bool vkey, bool fp8, bool mask, bool pair) {
   return s;
 }
 
+// fp8 K/V in frames of whole 64-key tiles with an odd number (>= 3) of
+// q-tiles per head runs as two launches: the first n_qtiles - 1 q-tiles of
+// every head as pair workgroups (each thread stages half of a K/V tile that
+// two q-tiles share), then the last q-tile of every head on the 4-wave
+// kernel, cut into key ranges so that its workgroups fill every slot (they
+// start on an empty GPU, so two per CU beat one), merged by the combine
+// kernel.  At 1152 queries over 4608 keys (B = 2, 32 heads) that is 256 pair
+// units in one round and 64 q-tiles in 8 ranges of 9 key tiles.  SplitPlan
+// holds both launches' split plans and their partial buffers' offsets.
+struct SplitPlan {
+  int64_t n_full[2];
+  int split[2];
+  int64_t off[2], bytes[2];
+  int64_t total;
+};
+
+inline SplitPlan plan_fp8_split_launch(int64_t B, int64_t H, int64_t nqt, int ntiles, int64_t D) {
+  SplitPlan sp{};
+  // launch 0: pair units over the first nqt - 1 q-tiles of every head
+  const int64_t nu0 = B * H * (nqt - 1) / 2;
+  plan_split(nu0, ntiles, flash_slots(D, false, true, false, true), &sp.n_full[0], &sp.split[0]);
+  sp.bytes[0] = sp.split[0] > 1 ? workspace_bytes_for((nu0 - sp.n_full[0]) * 2, sp.split[0], D) : 0;
+  // launch 1: the last q-tile of every head, one piece per slot
+  const int64_t nu1 = B * H;
+  const Slots s1 = flash_slots(D, false, true, false, false);
+  sp.n_full[1] = nu1;
+  sp.split[1] = 1;
+  if (s1.slots > 0 && nu1 < s1.slots) {
+    int k = (int)(s1.slots / nu1);
+    k = k > kMaxSplit ? kMaxSplit : k;
+    k = k > ntiles / 2 ? ntiles / 2 : k;   // pieces of >= 2 key tiles
+    if (k >= 2) {
+      sp.n_full[1] = 0;
+      sp.split[1] = k;
+    }
+  }
+  sp.bytes[1] = sp.split[1] > 1 ? workspace_bytes_for(nu1 - sp.n_full[1], sp.split[1], D) : 0;
+  sp.off[0] = 0;
+  sp.off[1] = round256(sp.bytes[0]);
+  sp.total = sp.off[1] + sp.bytes[1];
+  return sp;
+}
+
 extern "C" int ltx_flash_attn_workspace_size(int64_t B, int64_t Lq, int64_t H, int64_t D,
                                              int64_t* bytes) {
   clear_error();
@@ -1535,6 +1580,11 @@ extern "C" int ltx_flash_attn_workspace_size(int64_t B, int64_t Lq, int64_t H, i
     // with an unbounded key count the planned split is the largest any call of this shape plans
     plan_split(nu, 1 << 30, flash_slots(D, vk, f8, mk, kp), &n_full, &split);
     const int64_t b = split > 1 ? workspace_bytes_for((nu - n_full) * (kp ? 2 : 1), split, D) : 0;
+    need = b > need ? b : need;
+  }
+  // the two-launch fp8 plan for an odd q-tile count
+  if (nqt >= 3 && nqt % 2 == 1) {
+    const int64_t b = plan_fp8_split_launch(B, H, nqt, 1 << 30, D).total;
     need = b > need ? b : need;
   }
   *bytes = need;
@@ -1654,6 +1704,41 @@ static int flash_attn_fwd_impl(const void* q, int64_t B, int64_t Lq, int64_t H, 
   if (Lq == 0) return LTX_OK;
   LTX_REQUIRE(n > 0, "ltx_flash_attn_fwd: no keys (Lk == 0)");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // fp8 K/V, frames of whole tiles, an odd q-tile count >= 3: two launches
+  // (plan_fp8_split_launch), each over its own rows of q and out (q and out
+  // offset, Lq cut), so only without lse, whose rows are Lq apart.  A plan
+  // whose partials do not fit the workspace takes the one-launch path below.
+  if (fp8 && frame_tokens % kBN == 0 && p.n_qtiles >= 3 && p.n_qtiles % 2 == 1 && lse == nullptr &&
+      workspace != nullptr) {
+    const SplitPlan sp = plan_fp8_split_launch(B, H, p.n_qtiles, p.tile_start[n], D);
+    if (sp.total <= workspace_bytes) {
+      LTX_REQUIRE(al(workspace, 256), "ltx_flash_attn_fwd: workspace must be 256-byte aligned");
+      const int64_t lq0 = (int64_t)(p.n_qtiles - 1) * kBM;
+      FlashParams lp[2] = {p, p};
+      lp[0].Lq = (int)lq0;
+      lp[0].n_qtiles = p.n_qtiles - 1;
+      lp[0].pair = 1;
+      lp[1].q = p.q + lq0 * q_ls;
+      lp[1].o = p.o + lq0 * o_ls;
+      lp[1].o_al16 = ((uintptr_t)lp[1].o % 16 == 0 && o_bs % 8 == 0 && o_ls % 8 == 0 && o_hs % 8 == 0) ? 1 : 0;
+      lp[1].Lq = (int)(Lq - lq0);
+      lp[1].n_qtiles = 1;
+      lp[1].pair = 0;
+      for (int i = 0; i < 2; ++i) {
+        lp[i].n_full = (int)sp.n_full[i];
+        lp[i].split = sp.split[i];
+        if (sp.split[i] > 1) {
+          const int64_t tail = (i == 0 ? 2 * ((int64_t)B * H * lp[0].n_qtiles / 2 - sp.n_full[0])
+                                       : (int64_t)B * H - sp.n_full[1]);
+          lp[i].part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + sp.off[i]);
+          lp[i].part_o = reinterpret_cast<uint16_t*>(lp[i].part_ml + tail * sp.split[i] * kBM * 2);
+        }
+        const int rc = D == 128 ? launch_flash_pipe<128, true>(lp[i], st) : launch_flash_pipe<64, true>(lp[i], st);
+        if (rc != LTX_OK) return rc;
+      }
+      return LTX_OK;
+    }
+  }
   // balanced tail (needs a workspace; without one every q-tile runs whole).
   // Key-major bf16 V, or fp8 K/V in frames of whole 64-key tiles, with an
   // even number of q-tiles per head runs the pair kernel, whose grid counts

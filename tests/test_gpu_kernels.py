@@ -436,6 +436,41 @@ def test_flash_attn_bf16_vs_fp32(dev, case, vlayout):
     assert (lse.cpu() - torch.logsumexp(s_, -1)).abs().max().item() < 1e-2
 
 
+def test_flash_attn_fp8_odd_qtiles_lse_takes_one_launch(dev):
+    """fp8 K/V at 1152 queries (9 q-tiles per head): without lse the call runs
+    as two launches (pair workgroups, then the last q-tile of every head),
+    with lse as one (the 4-wave kernel, whose lse rows are Lq apart).  The
+    two agree to bf16 rounding (they cut different q-tiles into key ranges;
+    the rest run the same arithmetic and match bit for bit), and lse matches
+    the log-sum-exp of the dequantised logits."""
+    B, Lq, H, D, frame, lens = 2, 1152, 32, 128, 384, [384, 768, 1152]
+    g = gen(10)
+    q = randn((B, Lq, H, D), g, torch.bfloat16)
+    K = randn((B, sum(lens), H, D), g, torch.bfloat16)
+    V = randn((B, sum(lens), H, D), g, torch.bfloat16)
+    kc, ksc = OF.quantize_kv(K.float(), frame)
+    vc, vsc = OF.quantize_kv(V.float(), frame)
+    kd, vd, kscd, vscd = kc.to(dev), vc.to(dev), ksc.to(dev), vsc.to(dev)
+    segs, pos = [], 0
+    for n in lens:
+        f0, nf = pos // frame, n // frame
+        segs.append(KVSegment(kd[:, pos:pos + n], vd[:, pos:pos + n], kscd[:, :, f0:f0 + nf], vscd[:, :, f0:f0 + nf]))
+        pos += n
+    two = torch.empty(B, Lq, H, D, dtype=torch.bfloat16, device=dev)
+    one = torch.empty_like(two)
+    lse = torch.empty(B, H, Lq, dtype=torch.float32, device=dev)
+    kernels.flash_attn(q.to(dev), segs, two, frame_tokens=frame)
+    kernels.flash_attn(q.to(dev), segs, one, frame_tokens=frame, lse=lse)
+    torch.cuda.synchronize()
+    same = (two == one).float().mean().item()
+    print(f"fp8 odd q-tiles: two launches vs one: {same:.4f} of the outputs bit-identical", flush=True)
+    assert_bf16_close(two, one, "two launches vs one")
+    assert same >= 0.8, same
+    Kd = OF.dequantize_kv(kc, ksc, frame)
+    s_ = torch.einsum("bqhd,bkhd->bhqk", q.float(), Kd.float()) / math.sqrt(D)
+    assert (lse.cpu() - torch.logsumexp(s_, -1)).abs().max().item() < 1e-2
+
+
 @pytest.mark.parametrize("vlayout", ["token", "key"])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("scales", [(1, 6, 1, 12), (12, 1, 6, 1)], ids=["rising", "falling"])
@@ -506,10 +541,13 @@ def test_flash_attn_key_mask(dev):
                                   (1, 128, 4, 128, 64, [192]),
                                   (2, 96, 4, 64, 64, [64, 64, 64]),
                                   (2, 1280, 32, 128, 384, [384, 768, 1152]),
-                                  (1, 1024, 8, 64, 64, [256, 512, 1024])],
+                                  (1, 1024, 8, 64, 64, [256, 512, 1024]),
+                                  (1, 300, 8, 128, 64, [128, 256, 320]),
+                                  (2, 1152, 8, 64, 64, [256, 512, 1152])],
                          ids=["16x24grid", "64tok_frames", "8x12grid_96tok_frames", "8x12grid_96tok_D128",
                               "audio_25tok_frames", "1_tile", "2_tiles", "3_tiles", "3_segments_of_1_tile",
-                              "pair_split_tail_1280q", "pair_one_round_D64"])
+                              "pair_split_tail_1280q", "pair_one_round_D64", "odd_3_qtiles_partial_last",
+                              "odd_9_qtiles_D64"])
 def test_flash_attn_fp8_kv(dev, case):
     """fp8 K/V with one scale per (batch, head, frame); frames of 96 and 25
     tokens are cut into 64-key tiles at frame boundaries (64 + 32, and one
@@ -518,7 +556,10 @@ def test_flash_attn_fp8_kv(dev, case):
     with frames of whole tiles take the pair workgroups (group 0 stages K,
     group 1 V): 1280 queries at B = 2 and 32 heads give 320 units, 256 whole
     and 64 cut into key ranges and merged; 1024 queries over 8 heads one
-    partial round."""
+    partial round.  Odd q-tile counts >= 3 with frames of whole tiles run
+    the pair workgroups over all but the last q-tile of every head and then
+    the last ones, cut into key ranges, as a second launch: 1152 queries (9
+    q-tiles, D = 128 and 64) and 300 (3, the last one partial)."""
     B, Lq, H, D, frame, lens = case
     g = gen(9)
     q = randn((B, Lq, H, D), g, torch.bfloat16)

@@ -82,6 +82,9 @@ def _fp8_segments(dev, B, H, D, lens, frame, g):
     # fp8 K/V in 384-token frames, even q-tile counts per head (the pair
     # workgroups: group 0 stages K, group 1 V): 320 then 280 units on 256
     ((2, 1280, 32, 128, [384, 768, 1152]), (1, 1792, 40, 128, [384, 1152])),
+    # odd q-tile counts (9, then 11 per head): pair workgroups over all but
+    # the last q-tile of every head, then the last ones cut into key ranges
+    ((2, 1152, 32, 128, [384, 768, 1152]), (1, 1408, 40, 128, [384, 1152])),
 ])
 def test_noalloc_fp8_pair_matches_workspace_entry_point(dev, first, second):
     g = gen(22)

@@ -631,7 +631,8 @@ def fp8_step_bench(dev, steps: int, warmup: int, settle_seconds: float) -> dict:
     return {
         "query_tokens_per_s": B * LQ / (m["ms_step"] * 1e-3),
         "ms_per_step": m["ms_step"],
-        "attention": {"kernel": "flash_fwd_pipe_kernel<128, true> + flash_combine_kernel<128>",
+        "attention": {"kernel": "flash_fwd_pair_kernel<128, true> (q-tiles 0-7 of every head) + "
+                                "flash_fwd_pipe_kernel<128, true> (q-tile 8, key ranges) + flash_combine_kernel<128>",
                       "kernel_ms": m["ms_attn"], "kernel_ms_back_to_back": m["ms_attn_b2b"],
                       "tflops": ach, "frac_bf16_peak": ach / PEAK_BF16_TFLOPS,
                       "algorithmic_bytes": attn_bytes(1), "traffic": measured_traffic("fp8")},
@@ -795,7 +796,9 @@ def main():
                                "about 5 us the event before it adds); kernel_ms_back_to_back: K calls with "
                                "no other kernel between them, between two events",
                      "kernel": ("flash_fwd_pipe_kernel<128, false> + flash_combine_kernel<128>" if args.kv == "bf16"
-                                else "flash_fwd_pipe_kernel<128, true> + flash_combine_kernel<128>"),
+                                else "flash_fwd_pair_kernel<128, true> (q-tiles 0-7 of every head) + "
+                                     "flash_fwd_pipe_kernel<128, true> (q-tile 8, key ranges) + "
+                                     "flash_combine_kernel<128>"),
                      "kernel_ms": ms_attn,
                      "algorithmic_flops": fl, "algorithmic_bytes": attn_bytes(kvb)},
         "attention_tflops": ach,

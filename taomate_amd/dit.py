@@ -28,6 +28,7 @@ pair between them runs through this package's kernels.
 from __future__ import annotations
 
 import math
+import weakref
 from dataclasses import dataclass
 from typing import Dict, List, Optional, Tuple
 
@@ -461,6 +462,10 @@ def block_forward_with_cache(block: AVBlock, vx: torch.Tensor, ax: torch.Tensor,
     return vx, ax, new_cache
 
 
+# AVModel -> {device index: the stream its audio ops run on}
+_AUDIO_STREAMS: "weakref.WeakKeyDictionary[nn.Module, Dict[int, torch.cuda.Stream]]" = weakref.WeakKeyDictionary()
+
+
 def _tensors(x) -> Tuple[torch.Tensor, ...]:
     """The tensors of a RoPE table argument: a (cos, sin) pair, one tensor or None."""
     if x is None:
@@ -542,9 +547,11 @@ class AVModel(nn.Module):
         return self
 
     def _audio_stream_for(self, device: torch.device) -> Optional[torch.cuda.Stream]:
+        # kept outside the module's own attributes, so that copies and pickles
+        # of the model carry no stream (each copy makes its own on first use)
         if not getattr(self, "_overlap_audio", False) or device.type != "cuda":
             return None
-        streams = self.__dict__.setdefault("_audio_streams", {})
+        streams = _AUDIO_STREAMS.setdefault(self, {})
         if device.index not in streams:
             streams[device.index] = torch.cuda.Stream(device=device)
         return streams[device.index]

@@ -144,3 +144,22 @@ def test_per_frame_sigma_expands_to_tokens():
     assert D.AVModel._per_token(one, 12) is one
     with pytest.raises(ValueError):
         D.AVModel._per_token(t, 10)
+
+
+def test_audio_stream_switch_and_copies():
+    """The audio-stream overlap is on by default, off on the CPU (no stream
+    is made for a CPU device), switchable, and kept outside the module's
+    attributes: a deep copy or a state dict of the model carries no stream."""
+    import copy
+    cfg = D.AVConfig(num_layers=1, video_dim=64, audio_dim=64, video_heads=1, audio_heads=1, video_d_head=64,
+                     audio_d_head=64)
+    m = D.AVModel(cfg)
+    assert m._overlap_audio is True
+    assert m._audio_stream_for(torch.device("cpu")) is None
+    assert m.overlap_audio_(False) is m and m._overlap_audio is False
+    m.overlap_audio_()
+    m2 = copy.deepcopy(m)
+    assert m2._overlap_audio is True
+    assert not any(isinstance(v, dict) and v and all(hasattr(s, "cuda_stream") for s in v.values())
+                   for v in vars(m2).values())
+    assert set(m2.state_dict()) == set(m.state_dict())

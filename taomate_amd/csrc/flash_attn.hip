@@ -1819,8 +1819,9 @@ extern "C" int ltx_flash_attn_fwd(const void* q, int64_t B, int64_t Lq, int64_t 
 // 128 rows of (max, sum) in float32 and an O row in bf16).  The partial
 // results are at most two per CU (pieces <= resident slots, two 4-wave
 // workgroups per CU; the pair kernel's units hold two q-tiles at one
-// workgroup per CU), so a call needs at most 2 CUs x 128 x (8 + 2 D) bytes:
-// 17.3 MB for D = 128 at 256 CUs.  Every piece writes its whole partial before the
+// workgroup per CU), so a launch needs at most 2 CUs x 128 x (8 + 2 D) bytes:
+// 17.3 MB for D = 128 at 256 CUs (the fp8 two-launch plan keeps both
+// launches' partials in the array and is taken only when they fit).  Every piece writes its whole partial before the
 // combine kernel reads it, so nothing needs clearing between calls.  Each
 // device holds its own copy of the array for the life of the process; its
 // device address is looked up once per device (hipGetSymbolAddress) and
